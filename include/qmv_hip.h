@@ -1,0 +1,176 @@
+/*
+ * C ABI of the MI355X (gfx950) packed-weight matrix-vector library,
+ * libqmv_hip.so.
+ *
+ * Only plain C types cross this boundary: pointers, sizes, and the
+ * QmvTensorView descriptor below. A HIP stream is passed as void* (a
+ * hipStream_t; NULL selects the calling thread's own stream for host-pointer
+ * calls and the legacy default stream for device calls).
+ *
+ * Every function that returns int returns 1 on success and 0 on failure,
+ * like the reference's packed matvec (src/quantized_matvec.h:26-31). On
+ * failure qmv_last_error() returns a message for the calling thread. Output
+ * buffers are left untouched when validation fails; after a failed device
+ * operation their contents are unspecified.
+ *
+ * Thread safety: all entry points may be called concurrently from several
+ * host threads on the same registered weights (the reference's sessions do
+ * this, include/engine_api.h:10-17). Host-pointer calls use a per-thread HIP
+ * stream and per-thread staging buffers.
+ */
+#ifndef QMV_HIP_H
+#define QMV_HIP_H
+
+#include <stdint.h>
+#include "qmv_formats.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Borrowed descriptor of one packed 2-D GGUF tensor. Field for field the same
+ * layout and meaning as the reference's GgufQuantizedTensorView
+ * (src/gguf_reader.h:31-40): dimensions[0] = columns (K), dimensions[1] =
+ * rows (N); data is a host pointer with byte alignment only.
+ */
+typedef struct QmvTensorView {
+    const unsigned char *data;
+    uint32_t ggml_type;
+    uint32_t dimension_count;
+    uint64_t dimensions[4];
+    uint64_t element_count;
+    uint64_t block_elements;
+    uint64_t block_bytes;
+    uint64_t block_count;
+} QmvTensorView;
+
+/* ---- Drop-in host-pointer entry points -------------------------------- */
+
+/*
+ * output[N] = W[N,K] * input[K]. Replaces quantized_tensor_matvec_f32
+ * (src/quantized_matvec.h:32-38, src/quantized_matvec.cpp:86-162). Same
+ * argument rules: input_count == dimensions[0], output_count ==
+ * dimensions[1], type in {Q5_0, Q8_0, Q4_K, Q6_K}, consistent block layout.
+ * The packed tensor is uploaded to HBM on first use and cached (keyed by data
+ * pointer, type and shape, guarded by a sampled content fingerprint); input and
+ * output are host buffers.
+ */
+int qmv_tensor_matvec_f32(const QmvTensorView *matrix, const float *input,
+                          int input_count, float *output, int output_count);
+
+/*
+ * outputs[B,N] = inputs[B,K] * W^T for token-major batches. Replaces
+ * quantized_tensor_matmul_f32 (src/quantized_matvec.h:43-50,
+ * src/quantized_matvec.cpp:164-224). batch_count must be positive; the
+ * device kernels process up to QMV_MAX_BATCH positions per pass.
+ */
+int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs,
+                          int input_count, int batch_count, float *outputs,
+                          int output_count);
+
+#define QMV_MAX_BATCH 8
+
+/*
+ * Upload a packed tensor now (at model load) instead of on first use, so
+ * later matvec calls allocate nothing. No reference counterpart: the
+ * reference reads weights straight from its mmap (src/gguf_reader.cpp:695-697).
+ */
+int qmv_register_tensor(const QmvTensorView *matrix);
+
+/*
+ * Drop the device copies of every tensor whose host data pointer is data
+ * (call before the reference's gguf_close, src/gguf_reader.h:136-137).
+ * Returns the number of tensors released.
+ */
+int qmv_release_tensor(const unsigned char *data);
+void qmv_release_all(void);
+
+/*
+ * Decode rows [first_row, first_row + row_count) of a packed tensor on the
+ * GPU into output[row_count, K] (host memory). Bit-identical to the
+ * reference's per-block decoders q8_0/q5_0/q4_k/q6_k_dequantize_block
+ * (src/quantization.cpp:54-67,161-184,380-409,588-615) applied row by row.
+ */
+int qmv_dequantize_rows_f32(const QmvTensorView *matrix, int first_row,
+                            int row_count, float *output);
+
+/*
+ * Greedy argmax of host logits computed on the GPU. Same contract as
+ * sampler_greedy_sample (src/sampler.cpp:29-51): largest value, lowest id
+ * on exact ties, and failure (return 0, *token_id = -1) on any NaN/Inf or
+ * invalid argument.
+ */
+int qmv_greedy_sample_f32(const float *logits, int vocab_size, int *token_id);
+
+/* ---- Device-resident entry points ------------------------------------- */
+
+/* Opaque handle to a tensor resident in HBM in the tiled device layout. */
+typedef struct QmvDeviceTensor *qmv_device_tensor;
+
+/*
+ * Upload a packed host tensor into a new device tensor (validated like the
+ * matvec). The handle is independent of the host cache above and of the host
+ * data, which may be freed afterwards.
+ */
+int qmv_device_tensor_create(const QmvTensorView *matrix,
+                             qmv_device_tensor *out_tensor);
+void qmv_device_tensor_destroy(qmv_device_tensor tensor);
+
+/* Shape and storage of a device tensor; any output pointer may be NULL. */
+int qmv_device_tensor_info(qmv_device_tensor tensor, int *rows, int *columns,
+                           uint32_t *ggml_type, uint64_t *packed_bytes,
+                           uint64_t *device_bytes);
+
+/*
+ * d_outputs[B,N] = d_inputs[B,K] * W^T with device pointers, enqueued on
+ * stream without host synchronisation (1 <= batch_count <= QMV_MAX_BATCH).
+ */
+int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_inputs,
+                          int batch_count, float *d_outputs, void *stream);
+
+/*
+ * Several device tensors with the same column count and one shared input
+ * (q/k/v, or gate/up, of one layer) in a single launch. d_outputs[i] receives
+ * tensors[i]'s rows. count <= QMV_MAX_GROUP.
+ */
+#define QMV_MAX_GROUP 8
+int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count,
+                                const float *d_inputs, int batch_count,
+                                float *const *d_outputs, void *stream);
+
+/* Device decode of rows into d_output[row_count, K] (see qmv_dequantize_rows_f32). */
+int qmv_device_dequantize_f32(qmv_device_tensor tensor, int first_row,
+                              int row_count, float *d_output, void *stream);
+
+/*
+ * Greedy argmax over device logits. Writes d_result[0] = token id (or -1)
+ * and d_result[1] = 1 if every logit was finite, else 0.
+ */
+int qmv_device_greedy_argmax_f32(const float *d_logits, int vocab_size,
+                                 int *d_result, void *stream);
+
+/* ---- Library state ------------------------------------------------------ */
+
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char *qmv_last_error(void);
+
+/* Select the HIP device used by later calls from any thread (default 0). */
+int qmv_set_device(int ordinal);
+
+/* Number of HIP devices visible to the process (0 when none or no driver). */
+int qmv_device_count(void);
+
+/*
+ * Test hook for failure propagation (the role of the reference's link-time
+ * block-dot stubs, tests/quantized_matvec_failure_test.cpp:16-38): while
+ * armed, the next `count` host-pointer matvec/matmul calls fail after their
+ * kernel ran and before results are copied out. count = 0 disarms.
+ */
+void qmv_debug_fail_next_calls(int count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,54 @@
+/*
+ * Launch interface between the host shim and the gfx950 kernels.
+ */
+#ifndef QMV_KERNELS_H
+#define QMV_KERNELS_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmv_layout.h"
+
+#define QMV_MAX_WAVES 8
+#define QMV_MAX_JOBS 8
+
+namespace qmv {
+
+/* One tensor of a (possibly grouped) matvec launch. */
+struct MatvecJob {
+    const uint8_t *w;    /* tiled device layout */
+    float *y;            /* output, y[m * ldy + row] */
+    int rows;            /* N */
+    int ldy;
+    int tiles;           /* ceil(N / 64) */
+    int splits;          /* workgroups along K per tile */
+    int units_per_split; /* K-units per workgroup */
+    int wg_begin;        /* first workgroup id of this job in the grid */
+    int partial_offset;  /* float offset of this job's partials in the workspace */
+    int counter_offset;  /* offset of this job's per-tile arrival counters */
+};
+
+struct MatvecParams {
+    MatvecJob job[QMV_MAX_JOBS];
+    int njobs;
+    const float *x; /* x[m * ldx + k], shared by all jobs */
+    int ldx;
+    int cols;           /* K */
+    int units;          /* K-units per row */
+    int units_per_wave; /* contiguous K-units per wave */
+    float *partials;
+    unsigned *counters; /* all zero between launches */
+};
+
+hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
+hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
+                          int first_row, int row_count, hipStream_t s);
+hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
+                         int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
+                         hipStream_t s);
+hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,
+                         int *result, hipStream_t s);
+
+} // namespace qmv
+
+#endif

@@ -1,0 +1,956 @@
+/*
+ * gfx950 kernels of the packed-weight matrix-vector path.
+ *
+ * Mapping: one wavefront owns a 64-row tile (lane l = row l of the tile) and
+ * walks a contiguous range of K-units of that tile; a workgroup stacks up to
+ * 8 such waves along K and a launch may split K further across workgroups.
+ * Because every lane of a wave sits at the same K position, the activation
+ * values are wave-uniform: the compiler reads them with scalar loads into
+ * SGPRs and every FMA takes x as its SGPR operand, so x costs no VGPRs, no
+ * LDS and no per-lane traffic. Each lane accumulates its own row, so no
+ * cross-lane reduction is needed per row; waves of a workgroup combine
+ * through LDS, split workgroups through a workspace with a last-arriver
+ * reduction (both in fixed order, so results are run-to-run identical).
+ *
+ * Decode happens in registers from 16-byte plane loads (see qmv_layout.h):
+ * nibbles/bit-fields are isolated four at a time in the bytes of a dword and
+ * converted with byte-select conversions.
+ *   M == 1: affine terms are factored per scale group,
+ *           sum((a*q - b) x) = a*sum(q x) - b*sum(x),
+ *           with the group sums of x computed once per unit by the wave.
+ *   M >= 2: each weight is decoded exactly (bit-identical to the reference's
+ *           dequantisation) and reused for all M positions.
+ */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmv_kernels.h"
+
+namespace qmv {
+
+/* ---- small device helpers ----------------------------------------------- */
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits)
+{
+    const unsigned short s = (unsigned short)(bits & 0xffffu);
+    _Float16 h;
+    __builtin_memcpy(&h, &s, sizeof h);
+    return (float)h;
+}
+
+/* Byte k of v as a float; the backend selects the byte-select conversion. */
+__device__ __forceinline__ float ubyte(uint32_t v, int k)
+{
+    return (float)((v >> (8 * k)) & 0xffu);
+}
+
+__device__ __forceinline__ float sbyte(uint32_t v, int k)
+{
+    return (float)(int)(int8_t)((v >> (8 * k)) & 0xffu);
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float xor_sum(float v, int mask)
+{
+    return v + __shfl_xor(v, mask, 64);
+}
+
+/* Spread 4 bits b0..b3 to bit 4 of bytes 0..3 (fifth bit of Q5_0 codes). */
+__device__ __forceinline__ uint32_t spread_bits4(uint32_t b)
+{
+    return ((b * 0x00204081u) & 0x01010101u) << 4;
+}
+
+/* ---- per-format unit storage and loads ---------------------------------- */
+
+struct Q4KUnit { uint4 p[9]; };
+struct Q6KUnit { uint4 p[13]; uint32_t d; };
+struct Q80Unit { uint4 qs[8]; uint2 d; };
+struct Q50Unit { uint4 qs[4]; uint4 qh; uint2 d; };
+
+template <int FMT> struct UnitOf;
+template <> struct UnitOf<QMV_FMT_Q4_K> { using T = Q4KUnit; static constexpr int kBytes = 144, kWeights = 256; };
+template <> struct UnitOf<QMV_FMT_Q6_K> { using T = Q6KUnit; static constexpr int kBytes = 210, kWeights = 256; };
+template <> struct UnitOf<QMV_FMT_Q8_0> { using T = Q80Unit; static constexpr int kBytes = 136, kWeights = 128; };
+template <> struct UnitOf<QMV_FMT_Q5_0> { using T = Q50Unit; static constexpr int kBytes = 88, kWeights = 128; };
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *)p; }
+
+__device__ __forceinline__ void load_unit(Q4KUnit &u, const uint8_t *slab, int lane)
+{
+#pragma unroll
+    for (int p = 0; p < 9; ++p) u.p[p] = ld16(slab + p * 1024 + lane * 16);
+}
+
+__device__ __forceinline__ void load_unit(Q6KUnit &u, const uint8_t *slab, int lane)
+{
+#pragma unroll
+    for (int p = 0; p < 13; ++p) u.p[p] = ld16(slab + p * 1024 + lane * 16);
+    u.d = *(const unsigned short *)(slab + 13312 + lane * 2);
+}
+
+__device__ __forceinline__ void load_unit(Q80Unit &u, const uint8_t *slab, int lane)
+{
+#pragma unroll
+    for (int p = 0; p < 8; ++p) u.qs[p] = ld16(slab + p * 1024 + lane * 16);
+    u.d = *(const uint2 *)(slab + 8192 + lane * 8);
+}
+
+__device__ __forceinline__ void load_unit(Q50Unit &u, const uint8_t *slab, int lane)
+{
+#pragma unroll
+    for (int p = 0; p < 4; ++p) u.qs[p] = ld16(slab + p * 1024 + lane * 16);
+    u.qh = ld16(slab + 4096 + lane * 16);
+    u.d = *(const uint2 *)(slab + 5120 + lane * 8);
+}
+
+__device__ __forceinline__ uint32_t word(const uint4 &v, int e)
+{
+    return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ uint32_t word(const uint2 &v, int e) { return e == 0 ? v.x : v.y; }
+
+/* Activations are read through global-address-space pointers (so uniform
+ * reads become scalar loads). kGuard marks the partial last unit of a
+ * Q8_0/Q5_0 row: K is a multiple of 32, so it only lacks whole blocks, whose
+ * regions are skipped. */
+typedef const float __attribute__((address_space(1))) gfloat;
+
+/* Activation loads are ordered by data dependencies alone. The pointer of
+ * region p+1 is passed through an empty asm that also consumes one
+ * activation of region p (an SGPR) and the accumulators left by region p-1
+ * (VGPRs). So region p's scalar loads have landed before region p+1's are
+ * issued, region p-1's FMAs are done (its activations dead) before that, and
+ * no optimiser can merge, hoist or sink work across regions: at most two
+ * regions of activations are live in SGPRs. The result is still a uniform
+ * global pointer, so the loads stay scalar. */
+__device__ __forceinline__ gfloat *region_ptr(const float *p, float dep_s, float dep_v0, float dep_v1)
+{
+    gfloat *g = (gfloat *)p;
+    asm("" : "+s"(g) : "s"(dep_s), "v"(dep_v0), "v"(dep_v1));
+    return g;
+}
+
+/* A value that exists only once every acc[m] exists (an ordering token). */
+template <int M>
+__device__ __forceinline__ float all_of(const float (&acc)[M])
+{
+    float t = acc[0];
+#pragma unroll
+    for (int m = 1; m < M; ++m) asm("" : "+v"(t) : "v"(acc[m]));
+    return t;
+}
+
+/* A weight word that cannot be decoded before `dep` exists: ties the decode of
+ * region r to the accumulators of region r-1 so decodes are not hoisted. */
+__device__ __forceinline__ uint32_t after(uint32_t w, float dep)
+{
+    asm("" : "+v"(w) : "v"(dep));
+    return w;
+}
+
+/* Sum of the W/64 consecutive x values owned by this lane (W = unit width);
+ * shuffles then combine lanes into per-scale-group sums of x. */
+template <int W, bool kGuard>
+__device__ __forceinline__ float unit_x_partial(const float *__restrict__ xu, int lane, int kleft)
+{
+    if constexpr (W == 256) {
+        const int k = 4 * lane;
+        if (kGuard && k >= kleft) return 0.0f;
+        const float4 v = *(const float4 *)(xu + k);
+        return (v.x + v.y) + (v.z + v.w);
+    } else {
+        const int k = 2 * lane;
+        if (kGuard && k >= kleft) return 0.0f;
+        const float2 v = *(const float2 *)(xu + k);
+        return v.x + v.y;
+    }
+}
+
+/* ---- per-format regions --------------------------------------------------
+ * A region is a fixed set of weights of one unit together with the K index
+ * of each (all compile-time after unrolling). The M == 1 path uses 32-weight
+ * regions and factored scale groups; the M >= 2 path uses 8-weight regions of
+ * exactly decoded weights. */
+
+/* Q4_K header dwords: h0 = d | dmin << 16, h1 = scale bytes 0..3, h2 =
+ * 4..7, h3 = 8..11. Sub-block s < 4: sc = byte s of h1 & 63, m = byte s of
+ * h2 & 63; s >= 4: sc = (byte s-4 of h3 & 15) | (byte s-4 of h1 >> 6) << 4,
+ * m = (byte s-4 of h3 >> 4) | (byte s-4 of h2 >> 6) << 4. Plane 1 + 2g + h
+ * holds qs bytes 32g + 16h .. +15: low nibbles are weights 64g + 16h + i
+ * (sub-block 2g), high nibbles 64g + 32 + 16h + i (sub-block 2g + 1). The
+ * high nibble is used in place as 16*q (mask 0xF0) with 1/16 folded into its
+ * scale, which is exact. */
+struct Q4KScales { float a[8]; float m[8]; };
+
+__device__ __forceinline__ Q4KScales q4k_scales(const uint4 &h)
+{
+    const float d = f16_bits_to_f32(h.x);
+    const float dmin = f16_bits_to_f32(h.x >> 16);
+    const uint32_t sc_lo = h.y & 0x3f3f3f3fu;
+    const uint32_t m_lo = h.z & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    Q4KScales s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t scw = i < 4 ? sc_lo : sc_hi, mw = i < 4 ? m_lo : m_hi;
+        const float a = d * ubyte(scw, i & 3);
+        s.a[i] = (i & 1) ? a * 0.0625f : a; /* odd sub-blocks use 16*q codes */
+        s.m[i] = dmin * ubyte(mw, i & 3);
+    }
+    return s;
+}
+
+template <bool kGuard>
+__device__ __forceinline__ float q4k_m1(const Q4KUnit &u, const float *__restrict__ xu, int lane, int kleft)
+{
+    float xs = unit_x_partial<256, kGuard>(xu, lane, kleft);
+    xs = xor_sum(xs, 1); xs = xor_sum(xs, 2); xs = xor_sum(xs, 4); /* 8 lanes = 32 x */
+    /* Region p = plane 1+p: x runs [k0, k0+16) (low) and [k0+32, k0+48) (high). */
+    float xr[2][32];
+    auto load = [&](float (&dst)[32], int p, float ds, float v0, float v1) {
+        const int k0 = 64 * (p >> 1) + 16 * (p & 1);
+        gfloat *a = region_ptr(xu + k0, ds, v0, v1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            dst[i] = a[i];
+            dst[16 + i] = a[32 + i];
+        }
+    };
+    float slo[4] = {0.0f, 0.0f, 0.0f, 0.0f}, shi[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int g = p >> 1;
+        if (p < 7) {
+            const int gp = p > 0 ? (p - 1) >> 1 : 0;
+            load(xr[(p + 1) & 1], p + 1, xr[p & 1][0], slo[gp], shi[gp]);
+        }
+        const float(&x)[32] = xr[p & 1];
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t dw = word(u.p[1 + p], e);
+            const uint32_t lo = dw & 0x0f0f0f0fu, hi = dw & 0xf0f0f0f0u;
+            float &la = (e & 1) ? l1 : l0;
+            float &ha = (e & 1) ? h1 : h0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                la = fmaf(ubyte(lo, c), x[4 * e + c], la);
+                ha = fmaf(ubyte(hi, c), x[16 + 4 * e + c], ha);
+            }
+        }
+        slo[g] += l0 + l1;
+        shi[g] += h0 + h1;
+    }
+    const Q4KScales s = q4k_scales(u.p[0]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        acc = fmaf(s.a[2 * g], slo[g], acc);
+        acc = fmaf(s.a[2 * g + 1], shi[g], acc);
+        acc = fmaf(-s.m[2 * g], lane_value(xs, 16 * g), acc);
+        acc = fmaf(-s.m[2 * g + 1], lane_value(xs, 16 * g + 8), acc);
+    }
+    return acc;
+}
+
+/* Region r of 8 exactly decoded Q4_K weights: (g, h, e) = (r >> 3, r >> 2 & 1,
+ * r & 3); i < 4 low nibbles, i >= 4 high nibbles of dword e of plane 1+2g+h. */
+__device__ __forceinline__ int q4k_k(int r, int i)
+{
+    const int g = r >> 3, h = (r >> 2) & 1, e = r & 3;
+    return 64 * g + 16 * h + 4 * e + (i & 3) + (i >= 4 ? 32 : 0);
+}
+
+__device__ __forceinline__ void q4k_w(const Q4KUnit &u, const Q4KScales &s, int r, float (&w)[8], float dep)
+{
+    const int g = r >> 3, h = (r >> 2) & 1, e = r & 3;
+    const uint32_t dw = after(word(u.p[1 + 2 * g + h], e), dep);
+    const uint32_t lo = dw & 0x0f0f0f0fu, hi = dw & 0xf0f0f0f0u;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        /* a*q is exact, so the fused form rounds exactly like a*q - m. */
+        w[c] = fmaf(s.a[2 * g], ubyte(lo, c), -s.m[2 * g]);
+        w[4 + c] = fmaf(s.a[2 * g + 1], ubyte(hi, c), -s.m[2 * g + 1]);
+    }
+}
+
+/* Q6_K: weight n = 128g + 32r + o, low nibble from ql[64g + 32(r&1) + o]
+ * (>> 4 for r >= 2), two high bits from qh[32g + o] >> 2r, code q = low |
+ * high << 4 in 0..63, value (q - 32) * d * scales[n / 16]. For (g, half oh =
+ * o / 16) the planes are ql 4g+oh (r = 0, 2), ql 4g+2+oh (r = 1, 3) and qh
+ * 8+2g+oh; dword e covers o = 16oh + 4e .. +3. */
+__device__ __forceinline__ void q6k_codes(uint32_t qa, uint32_t qb, uint32_t qh, uint32_t (&q)[4])
+{
+    q[0] = (qa & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u);
+    q[1] = (qb & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u);
+    q[2] = ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u);
+    q[3] = ((qb >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ void q6k_dscales(const Q6KUnit &u, float (&dsc)[16])
+{
+    const float d = f16_bits_to_f32(u.d);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dsc[j] = d * sbyte(word(u.p[12], j >> 2), j & 3);
+}
+
+template <bool kGuard>
+__device__ __forceinline__ float q6k_m1(const Q6KUnit &u, const float *__restrict__ xu, int lane, int kleft)
+{
+    float xs = unit_x_partial<256, kGuard>(xu, lane, kleft);
+    xs = xor_sum(xs, 1); xs = xor_sum(xs, 2); /* 4 lanes = 16 x = one scale group */
+    /* Region p = (g, oh, rp): codes r = 2rp and 2rp+1 of dwords e = 0..3, i.e.
+     * x runs [k0, k0+16) and [k0+32, k0+48) with k0 = 128g + 64rp + 16oh. */
+    float xr[2][32];
+    auto load = [&](float (&dst)[32], int p, float ds, float v0, float v1) {
+        const int g = p >> 2, oh = (p >> 1) & 1, rp = p & 1;
+        const int k0 = 128 * g + 64 * rp + 16 * oh;
+        gfloat *a = region_ptr(xu + k0, ds, v0, v1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            dst[i] = a[i];
+            dst[16 + i] = a[32 + i];
+        }
+    };
+    float sg[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sg[j] = 0.0f;
+    load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int g = p >> 2, oh = (p >> 1) & 1, rp = p & 1;
+        if (p < 7) {
+            const int pp = p > 0 ? p - 1 : 0; /* region p-1's two scale groups */
+            const int jp = 8 * (pp >> 2) + 4 * (pp & 1) + ((pp >> 1) & 1);
+            load(xr[(p + 1) & 1], p + 1, xr[p & 1][0], sg[jp], sg[jp + 2]);
+        }
+        const float(&x)[32] = xr[p & 1];
+        float c00 = 0.0f, c01 = 0.0f, c10 = 0.0f, c11 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t qh = word(u.p[8 + 2 * g + oh], e);
+            uint32_t q0, q1;
+            if (rp == 0) {
+                q0 = (word(u.p[4 * g + oh], e) & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u);
+                q1 = (word(u.p[4 * g + 2 + oh], e) & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u);
+            } else {
+                q0 = ((word(u.p[4 * g + oh], e) >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u);
+                q1 = ((word(u.p[4 * g + 2 + oh], e) >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u);
+            }
+            float &a0 = (e & 1) ? c01 : c00;
+            float &a1 = (e & 1) ? c11 : c10;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                a0 = fmaf(ubyte(q0, c), x[4 * e + c], a0);
+                a1 = fmaf(ubyte(q1, c), x[16 + 4 * e + c], a1);
+            }
+        }
+        const int j0 = 8 * g + 4 * rp + oh; /* r = 2rp: j = 8g + 2r + oh */
+        sg[j0] += c00 + c01;
+        sg[j0 + 2] += c10 + c11;
+    }
+    float dsc[16];
+    q6k_dscales(u, dsc);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) /* scale group j covers x[16j .. 16j+15] */
+        acc = fmaf(dsc[j], fmaf(-32.0f, lane_value(xs, 4 * j), sg[j]), acc);
+    return acc;
+}
+
+/* Region r of 8 Q6_K weights: (g, oh, e, rp) with codes r' = 2rp, 2rp+1. */
+__device__ __forceinline__ int q6k_k(int r, int i)
+{
+    const int rp = r & 1, e = (r >> 1) & 3, oh = (r >> 3) & 1, g = r >> 4;
+    const int rr = 2 * rp + (i >> 2);
+    return 128 * g + 32 * rr + 16 * oh + 4 * e + (i & 3);
+}
+
+/* kSignedZeros: also reproduce the reference's sign of zero weights, (d*sc)*0
+ * keeps the sign of d*sc (the dequant kernel); the fused form below returns
+ * +0 there, which no sum can tell apart (the matvec paths). */
+template <bool kSignedZeros>
+__device__ __forceinline__ void q6k_w(const Q6KUnit &u, const float (&dsc)[16], int r, float (&w)[8], float dep)
+{
+    const int rp = r & 1, e = (r >> 1) & 3, oh = (r >> 3) & 1, g = r >> 4;
+    uint32_t q[4];
+    q6k_codes(after(word(u.p[4 * g + oh], e), dep), after(word(u.p[4 * g + 2 + oh], e), dep),
+              after(word(u.p[8 + 2 * g + oh], e), dep), q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int rr = 2 * rp + (i >> 2);
+        const float ds = dsc[8 * g + 2 * rr + oh];
+        /* ds*q and 32*ds are exact, so this is ds*(q-32) exactly. */
+        if (kSignedZeros) w[i] = ds * (ubyte(q[rr], i & 3) - 32.0f);
+        else w[i] = fmaf(ds, ubyte(q[rr], i & 3), -32.0f * ds);
+    }
+}
+
+/* Q8_0 unit = 4 blocks; signed codes are read as (q ^ 0x80) = q + 128. */
+__device__ __forceinline__ float q80_d(const Q80Unit &u, int j)
+{
+    return f16_bits_to_f32(word(u.d, j >> 1) >> (16 * (j & 1)));
+}
+
+template <bool kGuard>
+__device__ __forceinline__ float q80_m1(const Q80Unit &u, const float *__restrict__ xu, int lane, int kleft)
+{
+    float xs = unit_x_partial<128, kGuard>(xu, lane, kleft);
+    xs = xor_sum(xs, 1); xs = xor_sum(xs, 2); xs = xor_sum(xs, 4); xs = xor_sum(xs, 8); /* 16 lanes = 32 x */
+    float xr[2][32];
+    auto load = [&](float (&dst)[32], int j, float ds, float v0, float v1) {
+        gfloat *a = region_ptr(xu + 32 * j, ds, v0, v1);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = a[i];
+    };
+    /* K is a multiple of 32, so a partial last unit just lacks whole blocks. */
+    const int jvalid = kGuard ? kleft / 32 : 4;
+    float sj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < jvalid) { /* uniform; false only past K in a partial unit */
+            if (j + 1 < jvalid) load(xr[(j + 1) & 1], j + 1, xr[j & 1][0], sj[j > 0 ? j - 1 : 0], 0.0f);
+            const float(&x)[32] = xr[j & 1];
+            float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t dw = word(u.qs[2 * j + h], e) ^ 0x80808080u;
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc)
+                        c[2 * h + (e & 1)] = fmaf(ubyte(dw, cc), x[16 * h + 4 * e + cc], c[2 * h + (e & 1)]);
+                }
+            sj[j] = (c[0] + c[1]) + (c[2] + c[3]);
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(q80_d(u, j), fmaf(-128.0f, lane_value(xs, 16 * j), sj[j]), acc);
+    return acc;
+}
+
+/* Region r of 8 Q8_0 weights: (j, h, ep) = (r >> 2, r >> 1 & 1, r & 1). */
+__device__ __forceinline__ int q80_k(int r, int i) { return 8 * r + i; }
+
+template <bool kSignedZeros>
+__device__ __forceinline__ void q80_w(const Q80Unit &u, const float (&d)[4], int r, float (&w)[8], float dep)
+{
+    const int j = r >> 2, h = (r >> 1) & 1, ep = r & 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t dw = after(word(u.qs[2 * j + h], 2 * ep + (i >> 2)), dep) ^ 0x80808080u;
+        if (kSignedZeros) w[i] = d[j] * (ubyte(dw, i & 3) - 128.0f);
+        else w[i] = fmaf(d[j], ubyte(dw, i & 3), -128.0f * d[j]); /* d*(q+128) - 128d == d*q */
+    }
+}
+
+/* Q5_0 unit = 4 blocks. Block j: qs plane j (byte i: low nibble = weight i,
+ * high = weight i + 16), qh word j (bit i = fifth bit of weight i). Code q =
+ * nib | bit << 4 in 0..31, value d * (q - 16). */
+__device__ __forceinline__ void q50_codes(uint32_t dw, uint32_t qh, int e, uint32_t &lo, uint32_t &hi)
+{
+    lo = (dw & 0x0f0f0f0fu) | spread_bits4((qh >> (4 * e)) & 15u);
+    hi = ((dw >> 4) & 0x0f0f0f0fu) | spread_bits4((qh >> (16 + 4 * e)) & 15u);
+}
+
+__device__ __forceinline__ float q50_d(const Q50Unit &u, int j)
+{
+    return f16_bits_to_f32(word(u.d, j >> 1) >> (16 * (j & 1)));
+}
+
+template <bool kGuard>
+__device__ __forceinline__ float q50_m1(const Q50Unit &u, const float *__restrict__ xu, int lane, int kleft)
+{
+    float xs = unit_x_partial<128, kGuard>(xu, lane, kleft);
+    xs = xor_sum(xs, 1); xs = xor_sum(xs, 2); xs = xor_sum(xs, 4); xs = xor_sum(xs, 8);
+    float xr[2][32];
+    auto load = [&](float (&dst)[32], int j, float ds, float v0, float v1) {
+        gfloat *a = region_ptr(xu + 32 * j, ds, v0, v1);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) dst[i] = a[i];
+    };
+    /* K is a multiple of 32, so a partial last unit just lacks whole blocks. */
+    const int jvalid = kGuard ? kleft / 32 : 4;
+    float sj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < jvalid) { /* uniform; false only past K in a partial unit */
+            if (j + 1 < jvalid) load(xr[(j + 1) & 1], j + 1, xr[j & 1][0], sj[j > 0 ? j - 1 : 0], 0.0f);
+            const float(&x)[32] = xr[j & 1];
+            const uint32_t qh = word(u.qh, j);
+            float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t lo, hi;
+                q50_codes(word(u.qs[j], e), qh, e, lo, hi);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    c[e & 1] = fmaf(ubyte(lo, cc), x[4 * e + cc], c[e & 1]);
+                    c[2 + (e & 1)] = fmaf(ubyte(hi, cc), x[16 + 4 * e + cc], c[2 + (e & 1)]);
+                }
+            }
+            sj[j] = (c[0] + c[1]) + (c[2] + c[3]);
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(q50_d(u, j), fmaf(-16.0f, lane_value(xs, 16 * j), sj[j]), acc);
+    return acc;
+}
+
+/* Region r of 8 Q5_0 weights: (j, e) = (r >> 2, r & 3); i < 4 low, i >= 4 high. */
+__device__ __forceinline__ int q50_k(int r, int i)
+{
+    const int j = r >> 2, e = r & 3;
+    return 32 * j + 4 * e + (i & 3) + (i >= 4 ? 16 : 0);
+}
+
+template <bool kSignedZeros>
+__device__ __forceinline__ void q50_w(const Q50Unit &u, const float (&d)[4], int r, float (&w)[8], float dep)
+{
+    const int j = r >> 2, e = r & 3;
+    uint32_t lo, hi;
+    q50_codes(after(word(u.qs[j], e), dep), word(u.qh, j), e, lo, hi);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) { /* d*q and 16d are exact: d*(q-16) */
+        if (kSignedZeros) {
+            w[c] = d[j] * (ubyte(lo, c) - 16.0f);
+            w[4 + c] = d[j] * (ubyte(hi, c) - 16.0f);
+        } else {
+            w[c] = fmaf(d[j], ubyte(lo, c), -16.0f * d[j]);
+            w[4 + c] = fmaf(d[j], ubyte(hi, c), -16.0f * d[j]);
+        }
+    }
+}
+
+/* ---- format dispatch ------------------------------------------------------ */
+
+/* Per-unit decoded scales used by the exact (M >= 2 and dequant) paths. */
+template <int FMT> struct UnitScales;
+template <> struct UnitScales<QMV_FMT_Q4_K> { Q4KScales s; };
+template <> struct UnitScales<QMV_FMT_Q6_K> { float dsc[16]; };
+template <> struct UnitScales<QMV_FMT_Q8_0> { float d[4]; };
+template <> struct UnitScales<QMV_FMT_Q5_0> { float d[4]; };
+
+template <int FMT>
+__device__ __forceinline__ UnitScales<FMT> unit_scales(const typename UnitOf<FMT>::T &u)
+{
+    UnitScales<FMT> r;
+    if constexpr (FMT == QMV_FMT_Q4_K) r.s = q4k_scales(u.p[0]);
+    else if constexpr (FMT == QMV_FMT_Q6_K) q6k_dscales(u, r.dsc);
+    else if constexpr (FMT == QMV_FMT_Q8_0) { for (int j = 0; j < 4; ++j) r.d[j] = q80_d(u, j); }
+    else { for (int j = 0; j < 4; ++j) r.d[j] = q50_d(u, j); }
+    return r;
+}
+
+template <int FMT> struct RegionCount { static constexpr int value = UnitOf<FMT>::kWeights / 8; };
+
+template <int FMT>
+__device__ __forceinline__ int region_k(int r, int i)
+{
+    if constexpr (FMT == QMV_FMT_Q4_K) return q4k_k(r, i);
+    else if constexpr (FMT == QMV_FMT_Q6_K) return q6k_k(r, i);
+    else if constexpr (FMT == QMV_FMT_Q8_0) return q80_k(r, i);
+    else return q50_k(r, i);
+}
+
+/* Q4_K's fused decode already rounds (and signs zeros) exactly like the
+ * reference, so only the other formats distinguish kSignedZeros. */
+template <int FMT, bool kSignedZeros = false>
+__device__ __forceinline__ void region_w(const typename UnitOf<FMT>::T &u, const UnitScales<FMT> &s, int r,
+                                         float (&w)[8], float dep)
+{
+    if constexpr (FMT == QMV_FMT_Q4_K) q4k_w(u, s.s, r, w, dep);
+    else if constexpr (FMT == QMV_FMT_Q6_K) q6k_w<kSignedZeros>(u, s.dsc, r, w, dep);
+    else if constexpr (FMT == QMV_FMT_Q8_0) q80_w<kSignedZeros>(u, s.d, r, w, dep);
+    else q50_w<kSignedZeros>(u, s.d, r, w, dep);
+}
+
+template <int FMT, bool kGuard>
+__device__ __forceinline__ float unit_m1(const typename UnitOf<FMT>::T &u, const float *xu, int lane, int kleft)
+{
+    if constexpr (FMT == QMV_FMT_Q4_K) return q4k_m1<kGuard>(u, xu, lane, kleft);
+    else if constexpr (FMT == QMV_FMT_Q6_K) return q6k_m1<kGuard>(u, xu, lane, kleft);
+    else if constexpr (FMT == QMV_FMT_Q8_0) return q80_m1<kGuard>(u, xu, lane, kleft);
+    else return q50_m1<kGuard>(u, xu, lane, kleft);
+}
+
+/* Exact weights for all M positions, in 8-weight regions whose activations
+ * are two runs of 4 consecutive k per position. For small M the next
+ * region's activations load while this region computes (2 x 8M SGPRs);
+ * beyond that each region loads after the previous one finished. */
+template <int FMT, int M, bool kGuard>
+__device__ __forceinline__ void unit_mn(const typename UnitOf<FMT>::T &u, const float *__restrict__ xu, int ldx,
+                                        int kleft, float (&acc)[M])
+{
+    constexpr int R = RegionCount<FMT>::value;
+    constexpr bool kAhead = M <= 4;
+    const UnitScales<FMT> s = unit_scales<FMT>(u);
+    float xr[2][8 * M];
+    auto load = [&](float (&dst)[8 * M], int r, float ds, float v0, float v1) {
+        const int k0 = region_k<FMT>(r, 0), k1 = region_k<FMT>(r, 4);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            gfloat *a = region_ptr(xu + (size_t)m * ldx + k0, ds, v0, v1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dst[8 * m + i] = a[region_k<FMT>(r, i) - k0];
+                dst[8 * m + 4 + i] = a[region_k<FMT>(r, 4 + i) - k0];
+            }
+        }
+    };
+    /* Regions are ordered by block (4 per 32-weight block for Q8_0/Q5_0); a
+     * partial last unit lacks whole blocks, since K is a multiple of 32. */
+    const int rvalid = kGuard ? (kleft / 32) * 4 : R;
+    if (kAhead) load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r < rvalid) { /* uniform; false only past K in a partial unit */
+            const float prev = all_of(acc); /* every FMA of region r-1 is done */
+            if (kAhead) {
+                if (r + 1 < rvalid) load(xr[(r + 1) & 1], r + 1, xr[r & 1][0], prev, prev);
+            } else {
+                load(xr[r & 1], r, 0.0f, prev, prev);
+            }
+            float w[8];
+            region_w<FMT>(u, s, r, w, prev);
+            const float(&x)[8 * M] = xr[r & 1];
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[m] = fmaf(w[i], x[8 * m + i], acc[m]);
+        }
+    }
+}
+
+template <int FMT, int M>
+__device__ __forceinline__ void unit_step(const typename UnitOf<FMT>::T &u, const float *__restrict__ x, int ldx,
+                                          int cols, int unit, int lane, float (&acc)[M])
+{
+    constexpr int UW = UnitOf<FMT>::kWeights;
+    const int k0 = unit * UW;
+    const int kleft = cols - k0;
+    const float *xu = x + k0;
+    if (UW == 256 || kleft >= UW) {
+        if constexpr (M == 1) acc[0] += unit_m1<FMT, false>(u, xu, lane, kleft);
+        else unit_mn<FMT, M, false>(u, xu, ldx, kleft, acc);
+    } else {
+        if constexpr (M == 1) acc[0] += unit_m1<FMT, true>(u, xu, lane, kleft);
+        else unit_mn<FMT, M, true>(u, xu, ldx, kleft, acc);
+    }
+}
+
+/* ---- matvec kernel --------------------------------------------------------- */
+
+template <int FMT, int M>
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64)
+matvec_kernel(MatvecParams p)
+{
+    using Unit = typename UnitOf<FMT>::T;
+    constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    __shared__ float red[QMV_MAX_WAVES][M][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+
+    int j = 0;
+    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const MatvecJob &job = p.job[j];
+    const int local = blockIdx.x - job.wg_begin;
+    const int tile = local / job.splits;
+    const int split = local - tile * job.splits;
+
+    const int split_begin = split * job.units_per_split;
+    const int split_end = min(split_begin + job.units_per_split, p.units);
+    const int u_begin = split_begin + wave * p.units_per_wave;
+    const int u_end = min(u_begin + p.units_per_wave, split_end);
+
+    const uint8_t *wtile = job.w + (size_t)tile * p.units * SLAB;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+
+    if (u_begin < u_end) {
+        /* Two units in flight per wave: the next unit's planes are loading
+         * while the current one is decoded. */
+        Unit a, b;
+        load_unit(a, wtile + (size_t)u_begin * SLAB, lane);
+        for (int u = u_begin; u < u_end; u += 2) {
+            const bool has_b = u + 1 < u_end;
+            if (has_b) load_unit(b, wtile + (size_t)(u + 1) * SLAB, lane);
+            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u, lane, acc);
+            if (u + 2 < u_end) load_unit(a, wtile + (size_t)(u + 2) * SLAB, lane);
+            if (has_b) unit_step<FMT, M>(b, p.x, p.ldx, p.cols, u + 1, lane, acc);
+        }
+    }
+
+    /* Combine the waves of this workgroup in wave order. */
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
+    __syncthreads();
+    if (wave != 0) return;
+
+    float sum[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float s = red[0][m][lane];
+        for (int w = 1; w < nwaves; ++w) s += red[w][m][lane];
+        sum[m] = s;
+    }
+    const int row = tile * 64 + lane;
+
+    if (job.splits == 1) {
+        if (row < job.rows) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = sum[m];
+        }
+        return;
+    }
+
+    /* Split K: publish this split's partial, the last split to arrive adds
+     * all partials of the tile in split order. */
+    float *part = p.partials + job.partial_offset + ((size_t)tile * job.splits) * M * 64;
+#pragma unroll
+    for (int m = 0; m < M; ++m) part[((size_t)split * M + m) * 64 + lane] = sum[m];
+    __threadfence(); /* release: the partials are visible device-wide */
+    unsigned prev = 0;
+    if (lane == 0) prev = atomicAdd(p.counters + job.counter_offset + tile, 1u);
+    prev = __builtin_amdgcn_readlane(prev, 0);
+    if (prev != (unsigned)job.splits - 1u) return;
+    __threadfence(); /* acquire: see every other split's partials */
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float s = 0.0f;
+        for (int sp = 0; sp < job.splits; ++sp) {
+            const float v = part[((size_t)sp * M + m) * 64 + lane];
+            s = sp == 0 ? v : s + v;
+        }
+        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
+    }
+    if (lane == 0) p.counters[job.counter_offset + tile] = 0u;
+}
+
+/* ---- dequantisation kernel --------------------------------------------------
+ * One wave per (tile, unit); lane = row. Rows outside [first, first+count)
+ * and blocks past K are skipped. */
+template <int FMT>
+__global__ void __launch_bounds__(64)
+dequant_kernel(const uint8_t *__restrict__ w, float *__restrict__ out, int rows, int cols,
+               int units, int first_row, int row_count)
+{
+    using Unit = typename UnitOf<FMT>::T;
+    constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    constexpr int UW = UnitOf<FMT>::kWeights;
+    const int lane = threadIdx.x;
+    const int tile = blockIdx.y + first_row / 64;
+    const int unit = blockIdx.x;
+    const int row = tile * 64 + lane;
+    Unit u;
+    load_unit(u, w + ((size_t)tile * units + unit) * SLAB, lane);
+    if (row < first_row || row >= first_row + row_count || row >= rows) return;
+    float *dst = out + (size_t)(row - first_row) * cols + (size_t)unit * UW;
+    const int kleft = cols - unit * UW;
+    const UnitScales<FMT> s = unit_scales<FMT>(u);
+#pragma unroll
+    for (int r = 0; r < RegionCount<FMT>::value; ++r) {
+        float w[8];
+        region_w<FMT, true>(u, s, r, w, 0.0f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = region_k<FMT>(r, i);
+            if (UW == 256 || k < kleft) dst[k] = w[i];
+        }
+    }
+}
+
+/* ---- upload repack ----------------------------------------------------------
+ * Thread per (tile, unit, lane, block-in-unit): copies one packed block from
+ * the row-major GGUF bytes into its planes. */
+__device__ __forceinline__ size_t plane_offset(int fmt, int lane, int j, int i)
+{
+    switch (fmt) {
+    case QMV_FMT_Q4_K:
+        return (size_t)(i >> 4) * 1024 + lane * 16 + (i & 15);
+    case QMV_FMT_Q6_K:
+        return i < 208 ? (size_t)(i >> 4) * 1024 + lane * 16 + (i & 15) : 13312 + lane * 2 + (i - 208);
+    case QMV_FMT_Q8_0:
+        return i < 2 ? 8192 + lane * 8 + 2 * j + i
+                     : (size_t)(2 * j + ((i - 2) >> 4)) * 1024 + lane * 16 + ((i - 2) & 15);
+    default: /* Q5_0 */
+        return i < 2 ? 5120 + lane * 8 + 2 * j + i
+             : i < 6 ? 4096 + lane * 16 + 4 * j + (i - 2)
+                     : (size_t)j * 1024 + lane * 16 + (i - 6);
+    }
+}
+
+__global__ void repack_kernel(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int fmt,
+                              int rows, int blocks_per_row, int units, int blocks_per_unit,
+                              int block_bytes, int unit_bytes, long long total)
+{
+    const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int j = (int)(id % blocks_per_unit);
+    const long long r1 = id / blocks_per_unit;
+    const int lane = (int)(r1 & 63);
+    const long long r2 = r1 >> 6;
+    const int unit = (int)(r2 % units);
+    const long long tile = r2 / units;
+    const long long row = tile * 64 + lane;
+    const long long blk = (long long)unit * blocks_per_unit + j;
+    if (row >= rows || blk >= blocks_per_row) return;
+    const uint8_t *src = raw + (row * blocks_per_row + blk) * block_bytes;
+    uint8_t *slab = out + (tile * units + unit) * (size_t)unit_bytes * 64;
+    for (int i = 0; i < block_bytes; ++i) slab[plane_offset(fmt, lane, j, i)] = src[i];
+}
+
+/* ---- greedy argmax ----------------------------------------------------------
+ * Stage 1: each workgroup reduces a chunk to (max, lowest index) and counts
+ * non-finite values; stage 2: one workgroup combines in chunk order. */
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2)
+{
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+
+__global__ void __launch_bounds__(256)
+argmax_stage1(const float *__restrict__ logits, int n, float *__restrict__ bval, int *__restrict__ bidx,
+              int *__restrict__ bbad)
+{
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    __shared__ int sbad[256];
+    const int chunk = (n + gridDim.x - 1) / gridDim.x;
+    const int begin = blockIdx.x * chunk;
+    const int end = min(begin + chunk, n);
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    int bad = 0;
+    for (int i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        const float v = logits[i];
+        if (!isfinite(v)) { bad = 1; continue; }
+        argmax_merge(best, besti, v, i);
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = besti;
+    sbad[threadIdx.x] = bad;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            float v = sv[threadIdx.x];
+            int i = si[threadIdx.x];
+            argmax_merge(v, i, sv[threadIdx.x + s], si[threadIdx.x + s]);
+            sv[threadIdx.x] = v;
+            si[threadIdx.x] = i;
+            sbad[threadIdx.x] |= sbad[threadIdx.x + s];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        bval[blockIdx.x] = sv[0];
+        bidx[blockIdx.x] = si[0];
+        bbad[blockIdx.x] = sbad[0];
+    }
+}
+
+__global__ void __launch_bounds__(64)
+argmax_stage2(const float *__restrict__ bval, const int *__restrict__ bidx, const int *__restrict__ bbad,
+              int nblocks, int *__restrict__ result)
+{
+    if (threadIdx.x != 0) return;
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    int bad = 0;
+    for (int b = 0; b < nblocks; ++b) {
+        bad |= bbad[b];
+        argmax_merge(best, besti, bval[b], bidx[b]);
+    }
+    result[0] = bad || besti == 0x7fffffff ? -1 : besti;
+    result[1] = bad ? 0 : 1;
+}
+
+/* ---- host-side launchers -------------------------------------------------- */
+
+template <int FMT, int M>
+static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
+{
+    hipLaunchKernelGGL((matvec_kernel<FMT, M>), dim3(grid), dim3(waves * 64), 0, s, p);
+    return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t launch_matvec_f(const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
+{
+    switch (m) {
+    case 1: return launch_matvec_fm<FMT, 1>(p, grid, waves, s);
+    case 2: return launch_matvec_fm<FMT, 2>(p, grid, waves, s);
+    case 3: return launch_matvec_fm<FMT, 3>(p, grid, waves, s);
+    case 4: return launch_matvec_fm<FMT, 4>(p, grid, waves, s);
+    case 5: return launch_matvec_fm<FMT, 5>(p, grid, waves, s);
+    case 6: return launch_matvec_fm<FMT, 6>(p, grid, waves, s);
+    case 7: return launch_matvec_fm<FMT, 7>(p, grid, waves, s);
+    case 8: return launch_matvec_fm<FMT, 8>(p, grid, waves, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
+{
+    switch (fmt) {
+    case QMV_FMT_Q4_K: return launch_matvec_f<QMV_FMT_Q4_K>(p, m, grid, waves, s);
+    case QMV_FMT_Q6_K: return launch_matvec_f<QMV_FMT_Q6_K>(p, m, grid, waves, s);
+    case QMV_FMT_Q8_0: return launch_matvec_f<QMV_FMT_Q8_0>(p, m, grid, waves, s);
+    case QMV_FMT_Q5_0: return launch_matvec_f<QMV_FMT_Q5_0>(p, m, grid, waves, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
+                          int first_row, int row_count, hipStream_t s)
+{
+    if (row_count <= 0) return hipSuccess;
+    const int t0 = first_row / 64, t1 = (first_row + row_count - 1) / 64;
+    const dim3 grid(units, t1 - t0 + 1);
+    switch (fmt) {
+    case QMV_FMT_Q4_K: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q4_K>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
+    case QMV_FMT_Q6_K: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q6_K>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
+    case QMV_FMT_Q8_0: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q8_0>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
+    case QMV_FMT_Q5_0: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q5_0>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
+                         int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
+                         hipStream_t s)
+{
+    const long long total = (long long)tiles * units * 64 * blocks_per_unit;
+    const int threads = 256;
+    const long long grid = (total + threads - 1) / threads;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)grid), dim3(threads), 0, s, raw, out, fmt, rows,
+                       blocks_per_row, units, blocks_per_unit, block_bytes, unit_bytes, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,
+                         int *result, hipStream_t s)
+{
+    hipLaunchKernelGGL(argmax_stage1, dim3(nblocks), dim3(256), 0, s, logits, n, bval, bidx, bbad);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, s, bval, bidx, bbad, nblocks, result);
+    return hipGetLastError();
+}
+
+} // namespace qmv

@@ -1,0 +1,729 @@
+/*
+ * Host side of libqmv_hip.so: the C ABI declared in include/qmv_hip.h.
+ *
+ *  - Argument validation restated from the reference's dispatch
+ *    (src/quantized_matvec.cpp:93-149 for the matvec, :168-191 for the
+ *    batched form); every rule runs before any HIP call, so invalid calls
+ *    return 0 without touching the GPU.
+ *  - A thread-safe cache of device tensors keyed by (device, host data
+ *    pointer, type, shape), guarded by a sampled content fingerprint, so each
+ *    packed tensor is uploaded and re-tiled once (the reference reads the same
+ *    bytes from its mmap on every call).
+ *  - Per-thread HIP stream, pinned staging and device I/O buffers for the
+ *    host-pointer entry points (sessions call concurrently); a per-stream
+ *    workspace (split-K partials, arrival counters, argmax partials).
+ *  - Launch planning: tiles of 64 rows x K-units spread over waves,
+ *    workgroups and K-splits.
+ */
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <atomic>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "qmv_hip.h"
+#include "qmv_kernels.h"
+#include "qmv_layout.h"
+
+#define QMV_API extern "C" __attribute__((visibility("default")))
+
+struct QmvDeviceTensor {
+    int device;
+    uint32_t ggml_type;
+    QmvGeometry geo;
+    int rows, cols;
+    int blocks_per_row;
+    int units, tiles;
+    uint64_t packed_bytes, device_bytes;
+    uint8_t *data;
+};
+
+namespace {
+
+/* ---- errors ----------------------------------------------------------------- */
+
+thread_local std::string t_error;
+
+void set_error(const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_error = buf;
+}
+
+bool hip_ok(hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return true;
+    set_error("%s failed: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+#define HIP_TRY(expr)                         \
+    do {                                      \
+        if (!hip_ok((expr), #expr)) return 0; \
+    } while (0)
+
+std::atomic<int> g_device{0};
+std::atomic<int> g_fail_next{0};
+
+/* ---- validation (src/quantized_matvec.cpp:93-149, :168-191) ------------------ */
+
+struct Shape {
+    QmvGeometry geo;
+    int rows, cols, blocks_per_row;
+};
+
+bool view_layout_ok(const QmvTensorView *m, Shape *out)
+{
+    if (m == nullptr || m->data == nullptr) { set_error("null tensor view or data"); return false; }
+    if (m->dimension_count != 2) { set_error("tensor view must be 2-D"); return false; }
+    const uint64_t cols = m->dimensions[0], rows = m->dimensions[1];
+    if (cols == 0 || rows == 0 || cols > INT_MAX || rows > INT_MAX) {
+        set_error("tensor dimensions must be in 1..INT_MAX");
+        return false;
+    }
+    QmvGeometry g;
+    if (!qmv_geometry_of(m->ggml_type, &g)) {
+        set_error("unsupported ggml type %u (need Q5_0, Q8_0, Q4_K or Q6_K)", m->ggml_type);
+        return false;
+    }
+    if (m->block_elements != (uint64_t)g.block_elements || m->block_bytes != (uint64_t)g.block_bytes ||
+        cols % (uint64_t)g.block_elements != 0) {
+        set_error("block layout does not match the type or the column count");
+        return false;
+    }
+    const uint64_t bpr = cols / (uint64_t)g.block_elements;
+    if (bpr > UINT64_MAX / rows || m->block_count != bpr * rows || cols > UINT64_MAX / rows ||
+        m->element_count != cols * rows || m->block_count > SIZE_MAX / (uint64_t)g.block_bytes) {
+        set_error("element_count/block_count disagree with the shape");
+        return false;
+    }
+    out->geo = g;
+    out->rows = (int)rows;
+    out->cols = (int)cols;
+    out->blocks_per_row = (int)bpr;
+    return true;
+}
+
+bool matvec_args_ok(const QmvTensorView *m, const float *in, int in_count, const float *outp, int out_count,
+                    int batch, Shape *s)
+{
+    if (m == nullptr || in == nullptr || outp == nullptr || in_count <= 0 || out_count <= 0 || batch <= 0) {
+        set_error("null pointer or non-positive count");
+        return false;
+    }
+    if (!view_layout_ok(m, s)) return false;
+    if (in_count != s->cols || out_count != s->rows) {
+        set_error("input_count/output_count (%d, %d) do not match the tensor (%d cols, %d rows)", in_count,
+                  out_count, s->cols, s->rows);
+        return false;
+    }
+    if ((size_t)batch > SIZE_MAX / (size_t)in_count || (size_t)batch > SIZE_MAX / (size_t)out_count) {
+        set_error("batch size overflows");
+        return false;
+    }
+    return true;
+}
+
+/* ---- per-device / per-stream workspace --------------------------------------- */
+
+struct Workspace {
+    float *partials = nullptr;
+    size_t partial_cap = 0; /* floats */
+    unsigned *counters = nullptr;
+    size_t counter_cap = 0;
+    float *arg_val = nullptr;
+    int *arg_idx = nullptr;
+    int *arg_bad = nullptr;
+    int *arg_result = nullptr; /* 2 ints */
+    std::mutex mu;
+};
+
+/* Grow the workspace; waits for work already queued on the stream. */
+int workspace_reserve(Workspace &ws, hipStream_t stream, size_t partials, size_t counters)
+{
+    if (partials <= ws.partial_cap && counters <= ws.counter_cap) return 1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+        set_error("workspace must grow during stream capture; run the call once before capturing");
+        return 0;
+    }
+    HIP_TRY(hipStreamSynchronize(stream));
+    if (partials > ws.partial_cap) {
+        const size_t n = partials + partials / 2 + 4096;
+        if (ws.partials) HIP_TRY(hipFree(ws.partials));
+        ws.partials = nullptr;
+        ws.partial_cap = 0;
+        HIP_TRY(hipMalloc(&ws.partials, n * sizeof(float)));
+        ws.partial_cap = n;
+    }
+    if (counters > ws.counter_cap) {
+        const size_t n = counters + counters / 2 + 1024;
+        if (ws.counters) HIP_TRY(hipFree(ws.counters));
+        ws.counters = nullptr;
+        ws.counter_cap = 0;
+        HIP_TRY(hipMalloc(&ws.counters, n * sizeof(unsigned)));
+        HIP_TRY(hipMemset(ws.counters, 0, n * sizeof(unsigned)));
+        ws.counter_cap = n;
+    }
+    return 1;
+}
+
+constexpr int kArgBlocks = 512;
+
+int workspace_argmax(Workspace &ws)
+{
+    if (ws.arg_val) return 1;
+    HIP_TRY(hipMalloc(&ws.arg_val, kArgBlocks * sizeof(float)));
+    HIP_TRY(hipMalloc(&ws.arg_idx, kArgBlocks * sizeof(int)));
+    HIP_TRY(hipMalloc(&ws.arg_bad, kArgBlocks * sizeof(int)));
+    HIP_TRY(hipMalloc(&ws.arg_result, 2 * sizeof(int)));
+    return 1;
+}
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<Workspace>> g_workspaces;
+
+Workspace &workspace_for(int device, hipStream_t stream)
+{
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto &slot = g_workspaces[{device, stream}];
+    if (!slot) slot.reset(new Workspace());
+    return *slot;
+}
+
+/* ---- per-thread context for the host-pointer entry points -------------------- */
+
+struct HostCtx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    float *h_in = nullptr, *h_out = nullptr;
+    size_t h_in_cap = 0, h_out_cap = 0;
+    float *d_in = nullptr, *d_out = nullptr;
+    size_t d_in_cap = 0, d_out_cap = 0;
+};
+
+/* Contexts are never freed (HIP may already be torn down at process exit);
+ * a thread returns its context to a pool when it ends and new threads reuse it. */
+std::mutex g_pool_mu;
+std::vector<HostCtx *> g_pool;
+
+struct CtxHolder {
+    HostCtx *ctx = nullptr;
+    ~CtxHolder()
+    {
+        if (ctx) {
+            std::lock_guard<std::mutex> lock(g_pool_mu);
+            g_pool.push_back(ctx);
+        }
+    }
+};
+thread_local CtxHolder t_ctx;
+
+HostCtx *host_ctx()
+{
+    if (!t_ctx.ctx) {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        if (!g_pool.empty()) {
+            t_ctx.ctx = g_pool.back();
+            g_pool.pop_back();
+        } else {
+            t_ctx.ctx = new HostCtx();
+        }
+    }
+    HostCtx *c = t_ctx.ctx;
+    const int dev = g_device.load();
+    if (!hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+    if (c->device != dev) {
+        /* Fresh device: new stream and buffers (old ones stay with the old device). */
+        *c = HostCtx();
+        if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
+        c->device = dev;
+    }
+    return c;
+}
+
+int grow_pinned(float **p, size_t *cap, size_t n)
+{
+    if (n <= *cap) return 1;
+    if (*p) HIP_TRY(hipHostFree(*p));
+    *p = nullptr;
+    *cap = 0;
+    const size_t m = n + n / 2 + 1024;
+    HIP_TRY(hipHostMalloc((void **)p, m * sizeof(float), hipHostMallocDefault));
+    *cap = m;
+    return 1;
+}
+
+int grow_device(float **p, size_t *cap, size_t n)
+{
+    if (n <= *cap) return 1;
+    if (*p) HIP_TRY(hipFree(*p));
+    *p = nullptr;
+    *cap = 0;
+    const size_t m = n + n / 2 + 1024;
+    HIP_TRY(hipMalloc((void **)p, m * sizeof(float)));
+    *cap = m;
+    return 1;
+}
+
+/* ---- upload ------------------------------------------------------------------- */
+
+void tensor_free(QmvDeviceTensor *t)
+{
+    if (!t) return;
+    if (t->data) {
+        int cur = 0;
+        if (hipGetDevice(&cur) == hipSuccess && cur != t->device) {
+            if (hipSetDevice(t->device) == hipSuccess) {
+                (void)hipFree(t->data);
+                (void)hipSetDevice(cur);
+            }
+        } else {
+            (void)hipFree(t->data);
+        }
+    }
+    delete t;
+}
+
+int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_t stream, QmvDeviceTensor **out)
+{
+    std::unique_ptr<QmvDeviceTensor, void (*)(QmvDeviceTensor *)> t(new QmvDeviceTensor(), tensor_free);
+    t->device = device;
+    t->ggml_type = m->ggml_type;
+    t->geo = s.geo;
+    t->rows = s.rows;
+    t->cols = s.cols;
+    t->blocks_per_row = s.blocks_per_row;
+    t->units = (s.blocks_per_row + s.geo.blocks_per_unit - 1) / s.geo.blocks_per_unit;
+    t->tiles = (s.rows + QMV_TILE_ROWS - 1) / QMV_TILE_ROWS;
+    t->packed_bytes = (uint64_t)s.rows * (uint64_t)s.blocks_per_row * (uint64_t)s.geo.block_bytes;
+    t->device_bytes = (uint64_t)t->tiles * (uint64_t)t->units * QMV_TILE_ROWS * (uint64_t)s.geo.unit_bytes;
+    t->data = nullptr;
+
+    uint8_t *raw = nullptr;
+    HIP_TRY(hipMalloc(&raw, t->packed_bytes));
+    std::unique_ptr<uint8_t, hipError_t (*)(void *)> raw_guard(raw, hipFree);
+    HIP_TRY(hipMemcpyAsync(raw, m->data, t->packed_bytes, hipMemcpyHostToDevice, stream));
+    HIP_TRY(hipMalloc(&t->data, t->device_bytes));
+    if (t->device_bytes != t->packed_bytes) HIP_TRY(hipMemsetAsync(t->data, 0, t->device_bytes, stream));
+    HIP_TRY(qmv::launch_repack(s.geo.format, raw, t->data, s.rows, s.blocks_per_row, t->units,
+                               s.geo.blocks_per_unit, s.geo.block_bytes, s.geo.unit_bytes, t->tiles, stream));
+    HIP_TRY(hipStreamSynchronize(stream));
+    *out = t.release();
+    return 1;
+}
+
+/* Sampled fingerprint of the host bytes: catches a reused data pointer that
+ * now holds a different tensor (the reference's views die at gguf_close). */
+uint64_t fingerprint(const QmvTensorView *m, uint64_t bytes)
+{
+    uint64_t h = 0x9E3779B97F4A7C15ull ^ bytes;
+    const int samples = 64;
+    for (int i = 0; i < samples; ++i) {
+        uint64_t off = bytes <= 8 ? 0 : (bytes - 8) * (uint64_t)i / (uint64_t)(samples - 1);
+        uint64_t w = 0;
+        memcpy(&w, m->data + off, bytes < 8 ? bytes : 8);
+        h = (h ^ w) * 0x100000001b3ull;
+        h ^= h >> 29;
+    }
+    return h;
+}
+
+struct CacheEntry {
+    std::shared_ptr<QmvDeviceTensor> tensor;
+    uint64_t fp;
+};
+
+/* Heap-allocated and never destroyed: its entries free device memory, which
+ * must not happen during static destruction (HIP may be gone by then). */
+std::mutex g_cache_mu;
+auto &g_cache = *new std::map<std::tuple<int, const unsigned char *, uint32_t, int, int>, CacheEntry>();
+
+std::shared_ptr<QmvDeviceTensor> cached_tensor(const QmvTensorView *m, const Shape &s, HostCtx *c)
+{
+    const uint64_t bytes = (uint64_t)s.rows * (uint64_t)s.blocks_per_row * (uint64_t)s.geo.block_bytes;
+    const uint64_t fp = fingerprint(m, bytes);
+    const auto key = std::make_tuple(c->device, m->data, m->ggml_type, s.rows, s.cols);
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    auto it = g_cache.find(key);
+    if (it != g_cache.end() && it->second.fp == fp) return it->second.tensor;
+    QmvDeviceTensor *t = nullptr;
+    if (!tensor_upload(m, s, c->device, c->stream, &t)) return nullptr;
+    std::shared_ptr<QmvDeviceTensor> sp(t, tensor_free);
+    g_cache[key] = CacheEntry{sp, fp};
+    return sp;
+}
+
+/* ---- launch planning ------------------------------------------------------------- */
+
+int env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+struct Plan {
+    int units_per_wave, waves, splits, units_per_split;
+};
+
+/* Spread tiles x units over waves: aim for ~8 resident waves per CU across
+ * 256 CUs, at most 8 waves per workgroup, and split K across workgroups only
+ * as far as needed to fill the GPU. QMV_UNITS_PER_WAVE / QMV_WAVES override. */
+Plan plan_for(long long total_tiles, int units)
+{
+    static const int target = env_int("QMV_TARGET_WAVES", 2048);
+    static const int force_u = env_int("QMV_UNITS_PER_WAVE", 0);
+    static const int force_w = env_int("QMV_WAVES", 0);
+    const long long work = total_tiles * (long long)units;
+    int U = (int)((work + target - 1) / target);
+    U = U < 1 ? 1 : U > 8 ? 8 : U;
+    if (force_u > 0) U = force_u;
+    if (U > units) U = units;
+    int W = (units + U - 1) / U;
+    W = W < 1 ? 1 : W > QMV_MAX_WAVES ? QMV_MAX_WAVES : W;
+    if (force_w > 0 && force_w <= QMV_MAX_WAVES) W = force_w;
+    int S = (units + W * U - 1) / (W * U);
+    /* Rebalance so the splits are even. */
+    int ups = (units + S - 1) / S;
+    if (force_u <= 0) U = (ups + W - 1) / W;
+    if (force_w <= 0) W = (ups + U - 1) / U;
+    S = (units + ups - 1) / ups;
+    Plan p;
+    p.units_per_wave = U;
+    p.waves = W;
+    p.splits = S;
+    p.units_per_split = ups;
+    return p;
+}
+
+/* Enqueue one launch over `count` tensors sharing the input. */
+int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
+                 hipStream_t stream, Workspace &ws)
+{
+    const QmvDeviceTensor *t0 = ts[0];
+    long long total_tiles = 0;
+    for (int i = 0; i < count; ++i) total_tiles += ts[i]->tiles;
+    const Plan plan = plan_for(total_tiles, t0->units);
+
+    qmv::MatvecParams p;
+    memset(&p, 0, sizeof p);
+    p.njobs = count;
+    p.x = d_in;
+    p.ldx = t0->cols;
+    p.cols = t0->cols;
+    p.units = t0->units;
+    p.units_per_wave = plan.units_per_wave;
+    size_t partials = 0, counters = 0;
+    long long wg = 0;
+    for (int i = 0; i < count; ++i) {
+        qmv::MatvecJob &j = p.job[i];
+        j.w = ts[i]->data;
+        j.y = d_out[i];
+        j.rows = ts[i]->rows;
+        j.ldy = ts[i]->rows;
+        j.tiles = ts[i]->tiles;
+        j.splits = plan.splits;
+        j.units_per_split = plan.units_per_split;
+        j.wg_begin = (int)wg;
+        j.partial_offset = (int)partials;
+        j.counter_offset = (int)counters;
+        if (plan.splits > 1) {
+            partials += (size_t)ts[i]->tiles * plan.splits * batch * 64;
+            counters += (size_t)ts[i]->tiles;
+        }
+        wg += (long long)ts[i]->tiles * plan.splits;
+    }
+    if (wg > INT_MAX || partials > (size_t)INT_MAX || counters > (size_t)INT_MAX) {
+        set_error("launch too large");
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(ws.mu);
+    if (!workspace_reserve(ws, stream, partials, counters)) return 0;
+    p.partials = ws.partials;
+    p.counters = ws.counters;
+    HIP_TRY(qmv::launch_matvec(t0->geo.format, p, batch, (int)wg, plan.waves, stream));
+    return 1;
+}
+
+/* Batches of more than QMV_MAX_BATCH positions run as consecutive launches. */
+int launch_batched(QmvDeviceTensor *t, const float *d_in, int batch, float *d_out, hipStream_t stream,
+                   Workspace &ws)
+{
+    for (int b0 = 0; b0 < batch; b0 += QMV_MAX_BATCH) {
+        const int nb = batch - b0 < QMV_MAX_BATCH ? batch - b0 : QMV_MAX_BATCH;
+        float *out = d_out + (size_t)b0 * t->rows;
+        if (!launch_group(&t, 1, d_in + (size_t)b0 * t->cols, nb, &out, stream, ws)) return 0;
+    }
+    return 1;
+}
+
+int host_matmul(const QmvTensorView *m, const float *in, int in_count, int batch, float *out, int out_count)
+{
+    Shape s;
+    if (!matvec_args_ok(m, in, in_count, out, out_count, batch, &s)) return 0;
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    std::shared_ptr<QmvDeviceTensor> t = cached_tensor(m, s, c);
+    if (!t) return 0;
+    const size_t nin = (size_t)batch * (size_t)in_count, nout = (size_t)batch * (size_t)out_count;
+    if (!grow_pinned(&c->h_in, &c->h_in_cap, nin) || !grow_pinned(&c->h_out, &c->h_out_cap, nout) ||
+        !grow_device(&c->d_in, &c->d_in_cap, nin) || !grow_device(&c->d_out, &c->d_out_cap, nout))
+        return 0;
+    memcpy(c->h_in, in, nin * sizeof(float));
+    HIP_TRY(hipMemcpyAsync(c->d_in, c->h_in, nin * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    Workspace &ws = workspace_for(c->device, c->stream);
+    if (!launch_batched(t.get(), c->d_in, batch, c->d_out, c->stream, ws)) return 0;
+    HIP_TRY(hipMemcpyAsync(c->h_out, c->d_out, nout * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    int armed = g_fail_next.load();
+    while (armed > 0 && !g_fail_next.compare_exchange_weak(armed, armed - 1)) {
+    }
+    if (armed > 0) {
+        set_error("failure injected by qmv_debug_fail_next_calls");
+        return 0;
+    }
+    memcpy(out, c->h_out, nout * sizeof(float));
+    return 1;
+}
+
+} // namespace
+
+/* ---- C ABI ------------------------------------------------------------------------ */
+
+QMV_API int qmv_tensor_matvec_f32(const QmvTensorView *matrix, const float *input, int input_count,
+                                  float *output, int output_count)
+{
+    return host_matmul(matrix, input, input_count, 1, output, output_count);
+}
+
+QMV_API int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs, int input_count,
+                                  int batch_count, float *outputs, int output_count)
+{
+    return host_matmul(matrix, inputs, input_count, batch_count, outputs, output_count);
+}
+
+QMV_API int qmv_register_tensor(const QmvTensorView *matrix)
+{
+    Shape s;
+    if (!view_layout_ok(matrix, &s)) return 0;
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    return cached_tensor(matrix, s, c) ? 1 : 0;
+}
+
+QMV_API int qmv_release_tensor(const unsigned char *data)
+{
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    int n = 0;
+    for (auto it = g_cache.begin(); it != g_cache.end();) {
+        if (std::get<1>(it->first) == data) {
+            it = g_cache.erase(it);
+            ++n;
+        } else {
+            ++it;
+        }
+    }
+    return n;
+}
+
+QMV_API void qmv_release_all(void)
+{
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    g_cache.clear();
+}
+
+QMV_API int qmv_dequantize_rows_f32(const QmvTensorView *matrix, int first_row, int row_count, float *output)
+{
+    Shape s;
+    if (output == nullptr || !view_layout_ok(matrix, &s)) {
+        if (output == nullptr) set_error("null output");
+        return 0;
+    }
+    if (first_row < 0 || row_count <= 0 || (long long)first_row + row_count > s.rows) {
+        set_error("row range outside the tensor");
+        return 0;
+    }
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    std::shared_ptr<QmvDeviceTensor> t = cached_tensor(matrix, s, c);
+    if (!t) return 0;
+    const size_t n = (size_t)row_count * (size_t)s.cols;
+    if (!grow_device(&c->d_out, &c->d_out_cap, n)) return 0;
+    HIP_TRY(qmv::launch_dequant(t->geo.format, t->data, c->d_out, t->rows, t->cols, t->units, first_row, row_count,
+                                c->stream));
+    HIP_TRY(hipMemcpyAsync(output, c->d_out, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return 1;
+}
+
+QMV_API int qmv_device_greedy_argmax_f32(const float *d_logits, int vocab_size, int *d_result, void *stream)
+{
+    if (d_logits == nullptr || d_result == nullptr || vocab_size <= 0) {
+        set_error("invalid argmax arguments");
+        return 0;
+    }
+    int dev = g_device.load();
+    HIP_TRY(hipSetDevice(dev));
+    hipStream_t s = (hipStream_t)stream;
+    Workspace &ws = workspace_for(dev, s);
+    std::lock_guard<std::mutex> lock(ws.mu);
+    if (!workspace_argmax(ws)) return 0;
+    int blocks = (vocab_size + 4095) / 4096;
+    blocks = blocks < 1 ? 1 : blocks > kArgBlocks ? kArgBlocks : blocks;
+    HIP_TRY(qmv::launch_argmax(d_logits, vocab_size, ws.arg_val, ws.arg_idx, ws.arg_bad, blocks, d_result, s));
+    return 1;
+}
+
+QMV_API int qmv_greedy_sample_f32(const float *logits, int vocab_size, int *token_id)
+{
+    if (token_id) *token_id = -1;
+    if (logits == nullptr || token_id == nullptr || vocab_size <= 0) {
+        set_error("invalid greedy sampler arguments");
+        return 0;
+    }
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    const size_t n = (size_t)vocab_size;
+    if (!grow_device(&c->d_in, &c->d_in_cap, n) || !grow_device(&c->d_out, &c->d_out_cap, 2) ||
+        !grow_pinned(&c->h_out, &c->h_out_cap, 2))
+        return 0;
+    HIP_TRY(hipMemcpyAsync(c->d_in, logits, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    int *d_res = (int *)c->d_out;
+    if (!qmv_device_greedy_argmax_f32(c->d_in, vocab_size, d_res, c->stream)) return 0;
+    HIP_TRY(hipMemcpyAsync(c->h_out, d_res, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    int res[2];
+    memcpy(res, c->h_out, sizeof res);
+    if (res[1] != 1) {
+        set_error("greedy sampler received a non-finite logit");
+        return 0;
+    }
+    *token_id = res[0];
+    return 1;
+}
+
+QMV_API int qmv_device_tensor_create(const QmvTensorView *matrix, qmv_device_tensor *out_tensor)
+{
+    if (out_tensor == nullptr) {
+        set_error("null output handle");
+        return 0;
+    }
+    *out_tensor = nullptr;
+    Shape s;
+    if (!view_layout_ok(matrix, &s)) return 0;
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    QmvDeviceTensor *t = nullptr;
+    if (!tensor_upload(matrix, s, c->device, c->stream, &t)) return 0;
+    *out_tensor = t;
+    return 1;
+}
+
+QMV_API void qmv_device_tensor_destroy(qmv_device_tensor tensor)
+{
+    tensor_free(tensor);
+}
+
+QMV_API int qmv_device_tensor_info(qmv_device_tensor t, int *rows, int *columns, uint32_t *ggml_type,
+                                   uint64_t *packed_bytes, uint64_t *device_bytes)
+{
+    if (t == nullptr) {
+        set_error("null tensor");
+        return 0;
+    }
+    if (rows) *rows = t->rows;
+    if (columns) *columns = t->cols;
+    if (ggml_type) *ggml_type = t->ggml_type;
+    if (packed_bytes) *packed_bytes = t->packed_bytes;
+    if (device_bytes) *device_bytes = t->device_bytes;
+    return 1;
+}
+
+QMV_API int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count, const float *d_inputs,
+                                        int batch_count, float *const *d_outputs, void *stream)
+{
+    if (tensors == nullptr || d_inputs == nullptr || d_outputs == nullptr || count <= 0 ||
+        count > QMV_MAX_GROUP || batch_count <= 0 || batch_count > QMV_MAX_BATCH) {
+        set_error("invalid group matvec arguments");
+        return 0;
+    }
+    for (int i = 0; i < count; ++i) {
+        if (tensors[i] == nullptr || d_outputs[i] == nullptr) {
+            set_error("null tensor or output in group");
+            return 0;
+        }
+        if (tensors[i]->ggml_type != tensors[0]->ggml_type || tensors[i]->cols != tensors[0]->cols ||
+            tensors[i]->device != tensors[0]->device) {
+            set_error("grouped tensors must share type, column count and device");
+            return 0;
+        }
+    }
+    HIP_TRY(hipSetDevice(tensors[0]->device));
+    hipStream_t s = (hipStream_t)stream;
+    Workspace &ws = workspace_for(tensors[0]->device, s);
+    return launch_group(const_cast<QmvDeviceTensor *const *>(tensors), count, d_inputs, batch_count, d_outputs, s,
+                        ws);
+}
+
+QMV_API int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_inputs, int batch_count,
+                                  float *d_outputs, void *stream)
+{
+    return qmv_device_matvec_group_f32(&tensor, 1, d_inputs, batch_count, &d_outputs, stream);
+}
+
+QMV_API int qmv_device_dequantize_f32(qmv_device_tensor t, int first_row, int row_count, float *d_output,
+                                      void *stream)
+{
+    if (t == nullptr || d_output == nullptr || first_row < 0 || row_count <= 0 ||
+        (long long)first_row + row_count > t->rows) {
+        set_error("invalid dequantize arguments");
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(t->device));
+    HIP_TRY(qmv::launch_dequant(t->geo.format, t->data, d_output, t->rows, t->cols, t->units, first_row, row_count,
+                                (hipStream_t)stream));
+    return 1;
+}
+
+QMV_API const char *qmv_last_error(void)
+{
+    return t_error.c_str();
+}
+
+QMV_API int qmv_set_device(int ordinal)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || ordinal < 0 || ordinal >= n) {
+        set_error("device %d not available", ordinal);
+        return 0;
+    }
+    g_device.store(ordinal);
+    return 1;
+}
+
+QMV_API int qmv_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+QMV_API void qmv_debug_fail_next_calls(int count)
+{
+    g_fail_next.store(count > 0 ? count : 0);
+}

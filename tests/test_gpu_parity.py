@@ -1,0 +1,401 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+Bars (from the path's contract):
+  * dequantisation: bit-identical to the reference decoders (all bits,
+    including the sign of zero; NaN compared by class);
+  * matvec / matmul rows: |y - y_oracle| <= 1e-5 * sum_k |w_k x_k| per row,
+    y_oracle the scalar fp32 oracle, the sum in float64 (TOL below);
+  * greedy argmax: the same index as the CPU argmax (lowest id on ties).
+"""
+import ctypes
+import os
+import sys
+import threading
+
+import numpy as np
+import pytest
+
+import _blocks as B
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # relative to sum |w x| per row
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def check_rows(y, y_ref, absdot, what=""):
+    y = np.asarray(y, dtype=np.float64).ravel()
+    y_ref = np.asarray(y_ref, dtype=np.float64).ravel()
+    absdot = np.asarray(absdot, dtype=np.float64).ravel()
+    err = np.abs(y - y_ref)
+    bad = err > TOL * absdot
+    assert not bad.any(), (f"{what}: {bad.sum()} rows over tolerance; worst err/absdot "
+                           f"{np.max(err / np.maximum(absdot, 1e-300)):.3e} at row {int(np.argmax(err - TOL * absdot))}")
+    return float(np.max(err / np.maximum(absdot, 1e-300)))
+
+
+def matvec_parity(qmv, oracle, t, rows, cols, batch=1, seed=1, x=None, offset=0, what=""):
+    raw = qmv.synth_tensor(t, rows, cols, seed=seed)
+    if offset:
+        buf = np.zeros(raw.size + offset, dtype=np.uint8)
+        buf[offset:] = raw
+    else:
+        buf = raw
+    if x is None:
+        x = qmv.synth_normal(batch * cols, seed=seed + 1000).reshape(batch, cols)
+    v = qmv.make_view(buf, t, rows, cols, offset)
+    y = qmv.matvec(v, x if batch > 1 else x[0])
+    y = y.reshape(batch, rows)
+    y_ref = oracle.matvec(raw, t, rows, cols, x if batch > 1 else x[0]).reshape(batch, rows)
+    worst = 0.0
+    for b in range(batch):
+        _, absdot = oracle.row_stats(raw, t, rows, cols, x[b])
+        worst = max(worst, check_rows(y[b], y_ref[b], absdot, f"{what} pos {b}"))
+    log(f"{what} {B.BLOCK_BYTES and t} {rows}x{cols} M={batch}: worst err/sum|wx| = {worst:.2e}")
+    qmv.release_tensor(v.data)
+    return y
+
+
+# ---- dequantisation, bit for bit ----------------------------------------------------
+
+def _dequant_compare(qmv, oracle, raw, t, rows, cols, first=0, count=None, offset=0):
+    count = rows - first if count is None else count
+    buf = raw
+    if offset:
+        buf = np.zeros(raw.size + offset, dtype=np.uint8)
+        buf[offset:] = raw
+    v = qmv.make_view(buf, t, rows, cols, offset)
+    got = qmv.dequantize_rows(v, first, count)
+    exp = oracle.dequantize_rows(raw, t, rows, cols, first, count)
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+    qmv.release_tensor(v.data)
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+@pytest.mark.parametrize("rows,nblk", [(1, 1), (17, 3), (64, 4), (65, 5), (130, 9), (200, 16)])
+def test_dequant_bit_exact_random_blocks(qmv, oracle, gpu, t, rows, nblk):
+    """Random bytes with normal, subnormal, negative and zero fp16 scales;
+    row counts off the 64-row tile and (Q8_0/Q5_0) partial 4-block units."""
+    raw = B.raw_blocks(t, rows * nblk, seed=rows * 31 + nblk + t)
+    _dequant_compare(qmv, oracle, raw, t, rows, nblk * B.BLOCK_ELEMENTS[t], offset=1)
+
+
+def test_dequant_all_f16_scales(qmv, oracle, gpu):
+    """Every fp16 scale code through the device decoder (Q8_0 rows with
+    code r as scale and codes 1, 0, -1 in the first three weights)."""
+    rows = 65536
+    raw = np.zeros((rows, 34), dtype=np.uint8)
+    codes = np.arange(rows, dtype=np.uint16)
+    raw[:, 0] = codes & 0xFF
+    raw[:, 1] = codes >> 8
+    raw[:, 2] = 1
+    raw[:, 4] = 0xFF
+    _dequant_compare(qmv, oracle, raw.ravel(), B.Q8_0, rows, 32)
+
+
+@pytest.mark.parametrize("t,rows,cols", [
+    (B.Q8_0, 896, 896), (B.Q6_K, 896, 4864), (B.Q5_0, 1536, 1536), (B.Q5_0, 256, 1536),
+    (B.Q4_K, 8960, 1536), (B.Q4_K, 1536, 8960), (B.Q4_K, 3584, 3584), (B.Q4_K, 512, 3584),
+    (B.Q4_K, 18944, 3584), (B.Q6_K, 3584, 18944)])
+def test_dequant_bit_exact_config_shapes(qmv, oracle, gpu, t, rows, cols):
+    raw = qmv.synth_tensor(t, rows, cols, seed=rows + cols)
+    _dequant_compare(qmv, oracle, raw, t, rows, cols)
+
+
+def test_dequant_bit_exact_vocab_rows(qmv, oracle, gpu):
+    rows, cols = 151936, 3584
+    raw = qmv.synth_tensor(B.Q6_K, rows, cols, seed=4)
+    for first, count in ((0, 300), (75000, 129), (rows - 70, 70)):
+        _dequant_compare(qmv, oracle, raw, B.Q6_K, rows, cols, first, count)
+
+
+# ---- known answers through the drop-in ----------------------------------------------------
+
+def test_matvec_kats(qmv, gpu):
+    k = B.KATS["matvec_q8_0_two_rows"]
+    raw = np.frombuffer(b"".join(B.q8_0_block(bk["d"], bk["qs"]) for bk in k["blocks"]), dtype=np.uint8).copy()
+    v = qmv.make_view(raw, B.Q8_0, 2, 32)
+    assert list(qmv.matvec(v, B.sparse_vector(32, k["x"]))) == k["expected"]
+    one = B.sparse_vector(256, {"0": 1.0})
+    for t, blk, cols, key in (
+            (B.Q5_0, B.q5_0_block(0x3800, {}, {}), 32, "matvec_q5_0_single"),
+            (B.Q4_K, B.q4_k_block(0x3800, 0x3400, [1, 0, 0, 0, 1] + [0] * 7, {}), 256, "matvec_q4_k_single"),
+            (B.Q6_K, B.q6_k_block(0x3800, [1] + [0] * 15, 0, {}), 256, "matvec_q6_k_single")):
+        raw = np.frombuffer(blk, dtype=np.uint8).copy()
+        v = qmv.make_view(raw, t, 1, cols)
+        assert qmv.matvec(v, one[:cols])[0] == B.KATS[key]["expected"]
+    # single-block dot KATs as 1-row matrices
+    for t, blk, xs, key in ((B.Q8_0, B.kat_block("q8_0_dot"), B.KATS["q8_0_dot"]["x"], "q8_0_dot"),
+                            (B.Q5_0, B.kat_block("q5_0"), B.KATS["q5_0_dot"]["x"], "q5_0_dot"),
+                            (B.Q4_K, B.kat_block("q4_k"), B.KATS["q4_k_dot"]["x"], "q4_k_dot")):
+        raw = np.frombuffer(blk, dtype=np.uint8).copy()
+        n = B.BLOCK_ELEMENTS[t]
+        v = qmv.make_view(raw, t, 1, n)
+        assert abs(qmv.matvec(v, B.sparse_vector(n, xs))[0] - B.KATS[key]["expected"]) <= 1e-5
+    raw = np.frombuffer(B.kat_block("q6_k"), dtype=np.uint8).copy()
+    x = np.zeros(256, dtype=np.float32)
+    x[B.KATS["q6_k_dot"]["x_ones_at"]] = 1.0
+    assert abs(qmv.matvec(qmv.make_view(raw, B.Q6_K, 1, 256), x)[0] - B.KATS["q6_k_dot"]["expected"]) <= 1e-5
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_multirow_unaligned_with_sentinels(qmv, gpu, t):
+    """tests/quantized_matvec_reference_test.cpp:156-202: 17 rows x 3 blocks at
+    data+1, outputs written between two sentinels, results deterministic."""
+    rows, bpr, be, bb = 17, 3, B.BLOCK_ELEMENTS[t], B.BLOCK_BYTES[t]
+    cols = bpr * be
+    storage = np.zeros(1 + rows * bpr * bb, dtype=np.uint8)
+    vals = np.zeros((rows, bpr), dtype=np.float32)
+    for r in range(rows):
+        for b in range(bpr):
+            idx = r * bpr + b
+            blk, val = B.fixture_block(t, idx)
+            storage[1 + idx * bb:1 + (idx + 1) * bb] = np.frombuffer(blk, dtype=np.uint8)
+            vals[r, b] = val
+    x = ((np.arange(cols) % 13 - 6) / 8.0).astype(np.float32)
+    expected = np.array([sum(float(vals[r, b]) * float(x[b * be + c]) for b in range(bpr) for c in range(be))
+                         for r in range(rows)])
+    v = qmv.make_view(storage, t, rows, cols, offset=1)
+    out = np.full(rows + 2, -999.0, dtype=np.float32)
+    outv = out[1:-1]
+    assert qmv.quantized_tensor_matvec_f32(v, x, cols, outv, rows) == 1
+    assert out[0] == -999.0 and out[-1] == -999.0
+    assert np.all(np.abs(outv - expected) <= 1e-5)
+    again = np.empty(rows, dtype=np.float32)
+    assert qmv.quantized_tensor_matvec_f32(v, x, cols, again, rows) == 1
+    assert np.array_equal(again.view(np.uint32), outv.view(np.uint32))
+    qmv.release_tensor(v.data)
+
+
+def test_fixture_matvec_exact(qmv, gpu):
+    """tests/qwen2_weight_reference_test.cpp:152-181: 3 rows x 2 constant
+    blocks, input 1 then 2: every output exactly block_elements*(v0 + 2 v1)."""
+    for t in B.ALL_TYPES:
+        be, bb = B.BLOCK_ELEMENTS[t], B.BLOCK_BYTES[t]
+        storage = np.zeros(1 + 6 * bb, dtype=np.uint8)
+        vals = []
+        for b in range(6):
+            blk, val = B.fixture_block(t, b)
+            storage[1 + b * bb:1 + (b + 1) * bb] = np.frombuffer(blk, dtype=np.uint8)
+            vals.append(val)
+        x = np.where(np.arange(2 * be) < be, 1.0, 2.0).astype(np.float32)
+        y = qmv.matvec(qmv.make_view(storage, t, 3, 2 * be, offset=1), x)
+        for r in range(3):
+            assert y[r] == np.float32(be * (vals[2 * r] + 2 * vals[2 * r + 1])), (t, r)
+
+
+def test_invalid_arguments_leave_output(qmv, gpu):
+    raw = np.zeros(34, dtype=np.uint8)
+    v = qmv.make_view(raw, B.Q8_0, 1, 32)
+    x = np.zeros(32, dtype=np.float32)
+    y = np.full(2, -7.0, dtype=np.float32)
+    assert qmv.quantized_tensor_matvec_f32(v, x, 31, y, 1) == 0
+    assert qmv.quantized_tensor_matvec_f32(v, x, 32, y, 2) == 0
+    assert qmv.quantized_tensor_matmul_f32(v, x, 32, 0, y, 1) == 0
+    assert (y == -7.0).all()
+    raw = np.zeros(16, dtype=np.uint8)
+    v = qmv.make_view(raw, B.Q4_K, 4864, 896)  # config 2's Q4_K shape: K % 256 != 0
+    assert qmv.quantized_tensor_matvec_f32(v, np.zeros(896, np.float32), 896, np.zeros(4864, np.float32), 4864) == 0
+
+
+def test_failure_injection_publishes_nothing(qmv, gpu):
+    """Forced failure after the kernel: the call returns 0 and the caller's
+    output is untouched; the next call succeeds (the role of
+    tests/quantized_matvec_failure_test.cpp)."""
+    raw = qmv.synth_tensor(B.Q4_K, 64, 512, seed=3)
+    v = qmv.make_view(raw, B.Q4_K, 64, 512)
+    x = qmv.synth_normal(512, seed=4)
+    y = np.full(64, -99.0, dtype=np.float32)
+    qmv.hip_lib().qmv_debug_fail_next_calls(1)
+    assert qmv.quantized_tensor_matvec_f32(v, x, 512, y, 64) == 0
+    assert (y == -99.0).all()
+    assert "inject" in qmv.last_error()
+    assert qmv.quantized_tensor_matvec_f32(v, x, 512, y, 64) == 1
+    assert np.isfinite(y).all()
+    qmv.hip_lib().qmv_debug_fail_next_calls(0)
+
+
+# ---- parity at the workload shapes ----------------------------------------------------------
+
+def test_config1_q8_0_896(qmv, oracle, gpu):
+    x = qmv.synth_normal(896, seed=0).reshape(1, 896)
+    matvec_parity(qmv, oracle, B.Q8_0, 896, 896, seed=0, x=x, what="C1 Q8_0")
+
+
+def test_config2_q6_k_down(qmv, oracle, gpu):
+    matvec_parity(qmv, oracle, B.Q6_K, 896, 4864, seed=2, what="C2 Q6_K down")
+
+
+@pytest.mark.parametrize("t,rows,cols", [(B.Q5_0, 1536, 1536), (B.Q5_0, 256, 1536), (B.Q4_K, 8960, 1536),
+                                         (B.Q4_K, 1536, 8960)])
+def test_config3_prefill_m8(qmv, oracle, gpu, t, rows, cols):
+    matvec_parity(qmv, oracle, t, rows, cols, batch=8, seed=3, what="C3 M=8")
+
+
+@pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 3584, 3584), (B.Q4_K, 512, 3584), (B.Q4_K, 18944, 3584),
+                                         (B.Q6_K, 3584, 18944)])
+@pytest.mark.parametrize("batch", [1, 8])
+def test_config5_layer_shapes(qmv, oracle, gpu, t, rows, cols, batch):
+    matvec_parity(qmv, oracle, t, rows, cols, batch=batch, seed=5, what="C5")
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 6, 7, 8, 11])
+def test_every_batch_size(qmv, oracle, gpu, t, batch):
+    cols = 3 * B.BLOCK_ELEMENTS[t] if t in (B.Q4_K, B.Q6_K) else 7 * 32
+    matvec_parity(qmv, oracle, t, 200, cols, batch=batch, seed=batch, offset=1, what=f"batch {batch}")
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+@pytest.mark.parametrize("rows,cols", [(1, 256), (63, 512), (64, 1024), (65, 2304), (1000, 256 * 37)])
+def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
+    matvec_parity(qmv, oracle, t, rows, cols, seed=rows + cols, what="odd shape")
+
+
+def test_config4_vocab_projection_and_argmax(qmv, oracle, gpu):
+    """Q6_K 151936 x 3584 (446 MB) then greedy argmax: the index equals the
+    CPU argmax of the oracle's logits."""
+    rows, cols = 151936, 3584
+    raw = qmv.synth_tensor(B.Q6_K, rows, cols, seed=4)
+    x = qmv.synth_normal(cols, seed=44)
+    v = qmv.make_view(raw, B.Q6_K, rows, cols)
+    y = qmv.matvec(v, x)
+    y_ref = oracle.matvec(raw, B.Q6_K, rows, cols, x)
+    dot, absdot = oracle.row_stats(raw, B.Q6_K, rows, cols, x)
+    check_rows(y, y_ref, absdot, "C4")
+    ok_cpu, tok_cpu = oracle.greedy_argmax(y_ref)
+    ok_gpu, tok_gpu = qmv.greedy_sample(y)
+    assert ok_cpu == 1 and ok_gpu == 1
+    srt = np.sort(y_ref)
+    gap = float(srt[-1] - srt[-2])
+    bound = 2 * TOL * float(absdot[tok_cpu])
+    log(f"C4 argmax {tok_cpu}: top-2 gap {gap:.3e} vs row error bound {bound:.3e}")
+    assert tok_gpu == tok_cpu
+    assert qmv.greedy_sample(y_ref) == (1, tok_cpu)
+    qmv.release_tensor(v.data)
+
+
+def test_greedy_argmax_contract(qmv, gpu):
+    rng = np.random.default_rng(11)
+    for n in (1, 7, 4096, 4097, 151936, 1 << 21):
+        x = rng.standard_normal(n).astype(np.float32)
+        assert qmv.greedy_sample(x) == (1, int(np.argmax(x)))
+    x = np.zeros(100000, dtype=np.float32)
+    x[[777, 5000, 99999]] = 3.0
+    assert qmv.greedy_sample(x) == (1, 777)  # lowest id on ties
+    for bad in (np.nan, np.inf, -np.inf):
+        y = rng.standard_normal(5000).astype(np.float32)
+        y[4321] = bad
+        assert qmv.greedy_sample(y) == (0, -1)
+
+
+# ---- engine contracts ------------------------------------------------------------------------
+
+def test_deterministic_and_thread_safe(qmv, gpu):
+    """Bit-identical results run to run and from 4 concurrent host threads
+    sharing the same weights (sessions of include/engine_api.h:10-17)."""
+    t, rows, cols = B.Q4_K, 3584, 3584
+    raw = qmv.synth_tensor(t, rows, cols, seed=9)
+    v = qmv.make_view(raw, t, rows, cols)
+    xs = [qmv.synth_normal(cols, seed=100 + i) for i in range(4)]
+    ref = [qmv.matvec(v, x) for x in xs]
+    for i in range(4):
+        assert np.array_equal(qmv.matvec(v, xs[i]).view(np.uint32), ref[i].view(np.uint32))
+    errors = []
+
+    def worker(i):
+        try:
+            for _ in range(20):
+                y = qmv.matvec(v, xs[i])
+                if not np.array_equal(y.view(np.uint32), ref[i].view(np.uint32)):
+                    errors.append(i)
+        except Exception as e:  # pragma: no cover
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for h in th:
+        h.start()
+    for h in th:
+        h.join()
+    assert not errors
+    qmv.release_tensor(v.data)
+
+
+def test_cache_follows_new_contents(qmv, gpu):
+    """A host buffer reused for another tensor is re-uploaded: explicitly via
+    qmv_release_tensor, and by the content fingerprint otherwise."""
+    t, rows, cols = B.Q6_K, 256, 1024
+    buf = qmv.synth_tensor(t, rows, cols, seed=1)
+    v = qmv.make_view(buf, t, rows, cols)
+    x = qmv.synth_normal(cols, seed=2)
+    y1 = qmv.matvec(v, x)
+    buf[:] = qmv.synth_tensor(t, rows, cols, seed=2)
+    y2 = qmv.matvec(v, x)
+    assert not np.array_equal(y1, y2)
+    assert qmv.release_tensor(v.data) >= 1
+    buf[:] = qmv.synth_tensor(t, rows, cols, seed=1)
+    assert np.array_equal(qmv.matvec(v, x), y1)
+    assert qmv.register_tensor(v) == 1
+    qmv.release_all()
+
+
+def test_device_api_matches_host_api(qmv, gpu):
+    torch = pytest.importorskip("torch")
+    t, rows, cols = B.Q4_K, 18944, 3584
+    raw = qmv.synth_tensor(t, rows, cols, seed=21)
+    v = qmv.make_view(raw, t, rows, cols)
+    dt = qmv.DeviceTensor(v)
+    assert (dt.rows, dt.cols, dt.packed_bytes) == (rows, cols, raw.size)
+    x = qmv.synth_normal(8 * cols, seed=22).reshape(8, cols)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty((8, rows), device="cuda", dtype=torch.float32)
+    stream = torch.cuda.current_stream().cuda_stream
+    for m in (1, 8):
+        dt.matvec(dx.data_ptr(), m, dy.data_ptr(), stream)
+        torch.cuda.synchronize()
+        host = qmv.matvec(v, x[:m] if m > 1 else x[0]).reshape(m, rows)
+        assert np.array_equal(dy[:m].cpu().numpy().view(np.uint32), host.view(np.uint32))
+    # device dequant equals host dequant
+    out = torch.empty((5, cols), device="cuda", dtype=torch.float32)
+    dt.dequantize(100, 5, out.data_ptr(), stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), qmv.dequantize_rows(v, 100, 5).view(np.uint32))
+    dt.close()
+    qmv.release_all()
+
+
+def test_group_launch_matches_single(qmv, oracle, gpu):
+    """q/k/v sharing one input in one launch: each within tolerance of the oracle."""
+    torch = pytest.importorskip("torch")
+    cols = 3584
+    shapes = [(3584, 31), (512, 32), (512, 33)]
+    raws = [qmv.synth_tensor(B.Q4_K, r, cols, seed=s) for r, s in shapes]
+    dts = [qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, r, cols)) for raw, (r, _) in zip(raws, shapes)]
+    x = qmv.synth_normal(cols, seed=34)
+    dx = torch.from_numpy(x).cuda()
+    outs = [torch.empty(r, device="cuda", dtype=torch.float32) for r, _ in shapes]
+    qmv.device_matvec_group(dts, dx.data_ptr(), 1, [o.data_ptr() for o in outs],
+                            torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for raw, (r, _), o in zip(raws, shapes, outs):
+        y_ref = oracle.matvec(raw, B.Q4_K, r, cols, x)
+        _, absdot = oracle.row_stats(raw, B.Q4_K, r, cols, x)
+        check_rows(o.cpu().numpy(), y_ref, absdot, "group")
+    for d in dts:
+        d.close()
+
+
+def test_device_argmax(qmv, gpu):
+    torch = pytest.importorskip("torch")
+    x = np.random.default_rng(5).standard_normal(151936).astype(np.float32)
+    x[[10, 150000]] = 9.0
+    dx = torch.from_numpy(x).cuda()
+    res = torch.full((2,), -5, device="cuda", dtype=torch.int32)
+    qmv.device_greedy_argmax(dx.data_ptr(), x.size, res.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert res.cpu().tolist() == [10, 1]

@@ -1,0 +1,402 @@
+"""Pin the CPU oracle (oracle/qmv_oracle.c) before it is used to check the GPU.
+
+Each check is independent of the oracle's own code: the ldexp closed form
+and numpy's binary16 for f16, the reference tests' known-answer blocks,
+exact-rational decoders of the documented equations, the reference's LCG
+dot-vs-dequant trials, and bit-for-bit equality with the reference's own
+sources compiled into oracle/_ref (when that build exists).
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import _blocks as B
+
+pytestmark = []
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def _dq(oracle, t, blk):
+    fn = {B.Q8_0: "oracle_q8_0_dequantize_block", B.Q5_0: "oracle_q5_0_dequantize_block",
+          B.Q4_K: "oracle_q4_k_dequantize_block", B.Q6_K: "oracle_q6_k_dequantize_block"}[t]
+    out = np.empty(B.BLOCK_ELEMENTS[t], dtype=np.float32)
+    buf = np.frombuffer(bytes(blk), dtype=np.uint8).copy()
+    assert getattr(oracle.lib(), fn)(_p(buf), _p(out)) == 1
+    return out
+
+
+def _dot(oracle, t, blk, x):
+    fn = {B.Q8_0: "oracle_q8_0_dot_f32", B.Q5_0: "oracle_q5_0_dot_f32",
+          B.Q4_K: "oracle_q4_k_dot_f32", B.Q6_K: "oracle_q6_k_dot_f32"}[t]
+    buf = np.frombuffer(bytes(blk), dtype=np.uint8).copy()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    r = np.zeros(1, dtype=np.float32)
+    assert getattr(oracle.lib(), fn)(_p(buf), _p(x), _p(r)) == 1
+    return r[0]
+
+
+# ---- f16 ----------------------------------------------------------------------
+
+def test_f16_all_codes_closed_form(oracle):
+    """tests/q8_0_reference_test.cpp:48-64: every code vs ldexp, bit for bit."""
+    lib = oracle.lib()
+    out = np.array([lib.oracle_f16_to_f32(c) for c in range(65536)], dtype=np.float32)
+    codes = np.arange(65536)
+    exp5, frac = (codes >> 10) & 31, codes & 1023
+    finite = exp5 != 31
+    expected = np.where(exp5 == 0, np.ldexp(frac.astype(np.float64), -24),
+                        np.ldexp((1024 + frac).astype(np.float64), exp5.astype(np.int64) - 25))
+    expected = np.where(codes & 0x8000, -expected, expected).astype(np.float32)
+    assert np.array_equal(out[finite].view(np.uint32), expected[finite].view(np.uint32))
+    nan = (~finite) & (frac != 0)
+    inf = (~finite) & (frac == 0)
+    assert np.isnan(out[nan]).all()
+    assert np.isinf(out[inf]).all() and np.array_equal(np.signbit(out[inf]), (codes[inf] & 0x8000) != 0)
+    # numpy's own binary16 agrees too (including -0 and subnormals)
+    assert np.array_equal(out[finite].view(np.uint32),
+                          B.f16_values(codes[finite]).astype(np.float32).view(np.uint32))
+
+
+def test_f16_kats(oracle):
+    for code, val in B.KATS["f16"]:
+        assert oracle.lib().oracle_f16_to_f32(code) == np.float32(val)
+
+
+# ---- known-answer blocks (reference tests) --------------------------------------
+
+def test_q8_0_kats(oracle):
+    k = B.KATS
+    out = _dq(oracle, B.Q8_0, B.kat_block("q8_0_dequant"))
+    exp = B.sparse_vector(32, k["q8_0_dequant"]["expected"])
+    assert np.array_equal(out, exp)
+    x = B.sparse_vector(32, k["q8_0_dot"]["x"])
+    assert _dot(oracle, B.Q8_0, B.kat_block("q8_0_dot"), x) == k["q8_0_dot"]["expected"]
+
+
+def test_q5_0_kats(oracle):
+    k = B.KATS
+    out = _dq(oracle, B.Q5_0, B.kat_block("q5_0"))
+    exp = np.full(32, k["q5_0_dequant"]["default"], dtype=np.float32)
+    for i, v in k["q5_0_dequant"]["expected"].items():
+        exp[int(i)] = v
+    assert np.array_equal(out, exp)
+    x = B.sparse_vector(32, k["q5_0_dot"]["x"])
+    assert _dot(oracle, B.Q5_0, B.kat_block("q5_0"), x) == k["q5_0_dot"]["expected"]
+
+
+def test_q4_k_kats(oracle):
+    k = B.KATS
+    blk = np.frombuffer(B.kat_block("q4_k"), dtype=np.uint8).copy()
+    sc, mn = ctypes.c_uint8(), ctypes.c_uint8()
+    for s in range(8):
+        assert oracle.lib().oracle_q4_k_unpack_scale_min(_p(blk) + 4, s, ctypes.byref(sc), ctypes.byref(mn)) == 1
+        assert (sc.value, mn.value) == (k["q4_k_unpack"]["scales"][s], k["q4_k_unpack"]["mins"][s])
+    assert oracle.lib().oracle_q4_k_unpack_scale_min(_p(blk) + 4, 8, ctypes.byref(sc), ctypes.byref(mn)) == 0
+    assert oracle.lib().oracle_q4_k_unpack_scale_min(_p(blk) + 4, -1, ctypes.byref(sc), ctypes.byref(mn)) == 0
+    out = _dq(oracle, B.Q4_K, blk)
+    exp = np.repeat(np.array(k["q4_k_dequant"]["default_per_subblock"], dtype=np.float32), 32)
+    for i, v in k["q4_k_dequant"]["expected"].items():
+        exp[int(i)] = v
+    assert np.array_equal(out, exp)
+    x = B.sparse_vector(256, k["q4_k_dot"]["x"])
+    assert _dot(oracle, B.Q4_K, blk, x) == k["q4_k_dot"]["expected"]
+
+
+def test_q6_k_kats(oracle):
+    k = B.KATS
+    blk = np.frombuffer(B.kat_block("q6_k"), dtype=np.uint8).copy()
+    q, sc = ctypes.c_int8(), ctypes.c_int8()
+    for n, (idx, val) in enumerate(zip(k["q6_k_unpack"]["indices"], k["q6_k_unpack"]["values"])):
+        assert oracle.lib().oracle_q6_k_unpack_value(_p(blk), idx, ctypes.byref(q), ctypes.byref(sc)) == 1
+        assert (q.value, sc.value) == (val, n + 1)
+    assert oracle.lib().oracle_q6_k_unpack_value(_p(blk), 256, ctypes.byref(q), ctypes.byref(sc)) == 0
+    out = _dq(oracle, B.Q6_K, blk)
+    exp = np.empty(256, dtype=np.float32)
+    for n in range(256):
+        g, l = divmod(n, 128)
+        r, o = divmod(l, 32)
+        exp[n] = 0.5 * (8 * g + 2 * r + o // 16 + 1) * k["q6_k_dequant"]["default_per_region"][r]
+    for idx, val in zip(k["q6_k_dequant"]["selected"], k["q6_k_dequant"]["selected_values"]):
+        g, l = divmod(idx, 128)
+        r, o = divmod(l, 32)
+        exp[idx] = 0.5 * (8 * g + 2 * r + o // 16 + 1) * val
+    assert np.array_equal(out, exp)
+    x = np.zeros(256, dtype=np.float32)
+    x[k["q6_k_dot"]["x_ones_at"]] = 1.0
+    assert _dot(oracle, B.Q6_K, blk, x) == k["q6_k_dot"]["expected"]
+
+
+def test_block_null_arguments(oracle):
+    lib = oracle.lib()
+    buf = np.zeros(256, dtype=np.uint8)
+    out = np.zeros(256, dtype=np.float32)
+    for name in ("q8_0", "q5_0", "q4_k", "q6_k"):
+        assert getattr(lib, f"oracle_{name}_dequantize_block")(None, _p(out)) == 0
+        assert getattr(lib, f"oracle_{name}_dequantize_block")(_p(buf), None) == 0
+        assert getattr(lib, f"oracle_{name}_dot_f32")(None, _p(out), _p(out)) == 0
+        assert getattr(lib, f"oracle_{name}_dot_f32")(_p(buf), None, _p(out)) == 0
+        assert getattr(lib, f"oracle_{name}_dot_f32")(_p(buf), _p(out), None) == 0
+
+
+# ---- LCG dot-vs-dequant trials ------------------------------------------------------
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_lcg_dot_vs_dequant(oracle, t):
+    """128-trial randomized blocks of the reference tests, same tolerances."""
+    a, r = B.LCG_TOLERANCE[t]
+    for blk, x in B.lcg_trials(t):
+        w = _dq(oracle, t, blk)
+        expected = np.float32(0.0)
+        for i in range(len(x)):
+            expected = np.float32(expected + np.float32(w[i] * x[i]))
+        actual = _dot(oracle, t, blk, x)
+        assert abs(actual - expected) <= a + r * abs(expected)
+
+
+# ---- exact decoders of the documented equations --------------------------------------
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_dequant_matches_exact_decoder(oracle, t):
+    n = 24 if t == B.Q4_K else 200
+    raw = B.raw_blocks(t, n, seed=100 + t)
+    lcg = np.concatenate([blk for blk, _ in B.lcg_trials(t, 16)])
+    raw = np.concatenate([raw, lcg])
+    nb = raw.size // B.BLOCK_BYTES[t]
+    got = oracle.dequantize_rows(raw, t, nb, B.BLOCK_ELEMENTS[t], 0, nb)
+    exp = B.decode_exact(raw, t)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def _mistaken_decoders():
+    """Plausible slips in a decoder, planted in CPU-side copies of the oracle's
+    equations; each must disagree with the exact decoder on random blocks,
+    which shows that equality with it pins the oracle's index math."""
+    def q4k(raw, swap_halves=False, shift_scale=False, plus_min=False):
+        b = raw.reshape(-1, 144).astype(np.int64)
+        d = B.f16_values(b[:, 0] | (b[:, 1] << 8))
+        dm = B.f16_values(b[:, 2] | (b[:, 3] << 8))
+        p = b[:, 4:16]
+        out = np.empty((b.shape[0], 256))
+        for s in range(8):
+            ss = (s + 1) % 8 if shift_scale else s
+            if ss < 4:
+                sc, mn = p[:, ss] & 63, p[:, ss + 4] & 63
+            else:
+                sc = (p[:, ss + 4] & 15) | ((p[:, ss - 4] >> 6) << 4)
+                mn = (p[:, ss + 4] >> 4) | ((p[:, ss] >> 6) << 4)
+            half = (s % 2) ^ (1 if swap_halves else 0)
+            q = (b[:, 16 + 32 * (s // 2): 48 + 32 * (s // 2)] >> (4 * half)) & 15
+            out[:, 32 * s:32 * s + 32] = (d * sc)[:, None] * q + (1 if plus_min else -1) * (dm * mn)[:, None]
+        return out.astype(np.float32)
+
+    def q6k_no_half_offset(raw):
+        b = raw.reshape(-1, 210).astype(np.int64)
+        d = B.f16_values(b[:, 208] | (b[:, 209] << 8))
+        sc = b[:, 192:208].astype(np.uint8).view(np.int8).astype(np.float64)
+        idx = np.arange(256)
+        g, l = idx // 128, idx % 128
+        r, o = l // 32, l % 32
+        low = (b[:, 64 * g + 32 * (r % 2) + o] >> (4 * (r // 2))) & 15
+        high = (b[:, 128 + 32 * g + o] >> (2 * r)) & 3
+        return (d[:, None] * sc[:, 8 * g + 2 * r] * ((low | (high << 4)) - 32)).astype(np.float32)
+
+    def q50_bit_from_wrong_word(raw):
+        b = raw.reshape(-1, 22).astype(np.int64)
+        d = B.f16_values(b[:, 0] | (b[:, 1] << 8))
+        qh = b[:, 2] | (b[:, 3] << 8) | (b[:, 4] << 16) | (b[:, 5] << 24)
+        nib = np.concatenate([b[:, 6:22] & 15, b[:, 6:22] >> 4], axis=1)
+        bits = (qh[:, None] >> (np.arange(32) % 16)[None, :]) & 1
+        return (d[:, None] * (nib + 16 * bits - 16)).astype(np.float32)
+
+    return [
+        (B.Q4_K, lambda r: q4k(r, swap_halves=True)),
+        (B.Q4_K, lambda r: q4k(r, shift_scale=True)),
+        (B.Q4_K, lambda r: q4k(r, plus_min=True)),
+        (B.Q6_K, q6k_no_half_offset),
+        (B.Q5_0, q50_bit_from_wrong_word),
+    ]
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_exact_decoder_rejects_planted_mistakes(case):
+    t, wrong = _mistaken_decoders()[case]
+    raw = B.raw_blocks(t, 8, seed=900 + case)
+    exact = B.decode_exact(raw, t)
+    assert not np.array_equal(exact.view(np.uint32), wrong(raw).view(np.uint32))
+
+
+# ---- matvec contract ------------------------------------------------------------------
+
+def _fixture_matrix(t, rows, blocks_per_row, offset=1):
+    """Multi-row matrix of constant blocks at an unaligned address
+    (tests/quantized_matvec_reference_test.cpp:156-202)."""
+    bb, be = B.BLOCK_BYTES[t], B.BLOCK_ELEMENTS[t]
+    storage = np.zeros(offset + rows * blocks_per_row * bb, dtype=np.uint8)
+    vals = np.zeros((rows, blocks_per_row), dtype=np.float32)
+    for r in range(rows):
+        for b in range(blocks_per_row):
+            idx = r * blocks_per_row + b
+            blk, v = B.fixture_block(t, idx)
+            storage[offset + idx * bb: offset + (idx + 1) * bb] = np.frombuffer(blk, dtype=np.uint8)
+            vals[r, b] = v
+    return storage, vals
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_multirow_unaligned_matvec(oracle, t):
+    rows, bpr = 17, 3
+    be = B.BLOCK_ELEMENTS[t]
+    cols = bpr * be
+    storage, vals = _fixture_matrix(t, rows, bpr)
+    x = ((np.arange(cols) % 13 - 6) / 8.0).astype(np.float32)
+    expected = np.zeros(rows, dtype=np.float32)
+    for r in range(rows):
+        for b in range(bpr):
+            for c in range(be):
+                expected[r] = np.float32(expected[r] + np.float32(vals[r, b] * x[b * be + c]))
+    y = oracle.matvec(storage, t, rows, cols, x, offset=1)
+    assert np.all(np.abs(y - expected) <= 1e-5)
+
+
+def test_matvec_kats(oracle):
+    k = B.KATS["matvec_q8_0_two_rows"]
+    raw = np.frombuffer(b"".join(B.q8_0_block(bk["d"], bk["qs"]) for bk in k["blocks"]), dtype=np.uint8).copy()
+    x = B.sparse_vector(32, k["x"])
+    assert list(oracle.matvec(raw, B.Q8_0, 2, 32, x)) == k["expected"]
+    one = B.sparse_vector(256, {"0": 1.0})
+    raw = np.frombuffer(B.q5_0_block(0x3800, {}, {}), dtype=np.uint8).copy()
+    assert oracle.matvec(raw, B.Q5_0, 1, 32, one[:32])[0] == B.KATS["matvec_q5_0_single"]["expected"]
+    raw = np.frombuffer(B.q4_k_block(0x3800, 0x3400, [1, 0, 0, 0, 1] + [0] * 7, {}), dtype=np.uint8).copy()
+    assert oracle.matvec(raw, B.Q4_K, 1, 256, one)[0] == B.KATS["matvec_q4_k_single"]["expected"]
+    raw = np.frombuffer(B.q6_k_block(0x3800, [1] + [0] * 15, 0, {}), dtype=np.uint8).copy()
+    assert oracle.matvec(raw, B.Q6_K, 1, 256, one)[0] == B.KATS["matvec_q6_k_single"]["expected"]
+
+
+def test_matmul_equals_repeated_matvec(oracle):
+    rng = np.random.default_rng(7)
+    for t in B.ALL_TYPES:
+        rows, cols = 9, 2 * B.BLOCK_ELEMENTS[t]
+        raw = B.raw_blocks(t, rows * 2, seed=t)
+        x = rng.standard_normal((5, cols)).astype(np.float32)
+        ym = oracle.matvec(raw, t, rows, cols, x)
+        for b in range(5):
+            assert np.array_equal(ym[b], oracle.matvec(raw, t, rows, cols, x[b]))
+
+
+def test_invalid_arguments(oracle):
+    """tests/quantized_matvec_reference_test.cpp:223-259 plus the layout rules."""
+    lib = oracle.lib()
+    raw = np.zeros(34, dtype=np.uint8)
+    x = np.zeros(32, dtype=np.float32)
+    y = np.zeros(2, dtype=np.float32)
+    v = oracle.view(raw, B.Q8_0, 1, 32)
+    vp = ctypes.byref(v)
+    assert lib.oracle_matvec_f32(None, _p(x), 32, _p(y), 1) == 0
+    assert lib.oracle_matvec_f32(vp, None, 32, _p(y), 1) == 0
+    assert lib.oracle_matvec_f32(vp, _p(x), 32, None, 1) == 0
+    assert lib.oracle_matvec_f32(vp, _p(x), 31, _p(y), 1) == 0
+    assert lib.oracle_matvec_f32(vp, _p(x), 32, _p(y), 2) == 0
+    assert lib.oracle_matmul_f32(vp, _p(x), 32, 0, _p(y), 1) == 0
+    for field, value in (("dimension_count", 1), ("ggml_type", 99), ("block_count", 0),
+                         ("block_elements", 33), ("block_bytes", 35), ("element_count", 31)):
+        w = oracle.view(raw, B.Q8_0, 1, 32)
+        setattr(w, field, value)
+        assert lib.oracle_matvec_f32(ctypes.byref(w), _p(x), 32, _p(y), 1) == 0
+    assert lib.oracle_matvec_f32(vp, _p(x), 32, _p(y), 1) == 1
+
+
+def test_config2_q4_k_shape_is_rejected(oracle):
+    """Q4_K 4864 x 896: 896 is not a multiple of 256 (src/quantized_matvec.cpp:136-138)."""
+    raw = np.zeros(1, dtype=np.uint8)
+    v = oracle.view(raw, B.Q4_K, 4864, 896)
+    v.block_count = 4864 * 896 // 256
+    x = np.zeros(896, dtype=np.float32)
+    y = np.zeros(4864, dtype=np.float32)
+    assert oracle.lib().oracle_matvec_f32(ctypes.byref(v), _p(x), 896, _p(y), 4864) == 0
+
+
+def test_greedy_argmax(oracle):
+    assert oracle.greedy_argmax(np.array([1, 3, 3, 2], dtype=np.float32)) == (1, 1)
+    assert oracle.greedy_argmax(np.array([-5], dtype=np.float32)) == (1, 0)
+    assert oracle.greedy_argmax(np.array([1, np.nan, 3], dtype=np.float32)) == (0, -1)
+    assert oracle.greedy_argmax(np.array([1, np.inf], dtype=np.float32)) == (0, -1)
+    x = np.random.default_rng(3).standard_normal(100000).astype(np.float32)
+    assert oracle.greedy_argmax(x) == (1, int(np.argmax(x)))
+
+
+# ---- the reference itself, compiled from its sources ---------------------------------------
+
+def _ref_or_skip(oracle, kind):
+    lib = oracle.ref_lib(kind)
+    if lib is None:
+        pytest.skip("oracle/_ref not built (the reference checkout is absent on this host)")
+    return lib
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_oracle_bit_identical_to_reference_scalar_build(oracle, t):
+    """Dequant and block dots bit-for-bit equal to the reference's scalar
+    branches; matvec/matmul bit-for-bit equal to its row loop."""
+    ref = _ref_or_skip(oracle, "scalar")
+    name = {B.Q8_0: "q8_0", B.Q5_0: "q5_0", B.Q4_K: "q4_k", B.Q6_K: "q6_k"}[t]
+    be = B.BLOCK_ELEMENTS[t]
+    raw = B.raw_blocks(t, 64, seed=200 + t)
+    rng = np.random.default_rng(t)
+    for i in range(64):
+        blk = raw[i * B.BLOCK_BYTES[t]:(i + 1) * B.BLOCK_BYTES[t]].copy()
+        ours = _dq(oracle, t, blk)
+        theirs = np.empty(be, dtype=np.float32)
+        assert getattr(ref, f"ref_{name}_dequantize_block")(_p(blk), _p(theirs)) == 1
+        assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+        x = rng.standard_normal(be).astype(np.float32)
+        r = np.zeros(1, dtype=np.float32)
+        assert getattr(ref, f"ref_{name}_dot_f32")(_p(blk), _p(x), _p(r)) == 1
+        assert np.float32(_dot(oracle, t, blk, x)).view(np.uint32) == r.view(np.uint32)[0]
+    rows, cols = 13, 4 * be
+    raw = B.raw_blocks(t, rows * 4, seed=300 + t)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    v = oracle.view(raw, t, rows, cols)
+    for m in (1, 3):
+        theirs = np.empty((m, rows), dtype=np.float32)
+        if m == 1:
+            assert ref.ref_quantized_tensor_matvec_f32(ctypes.byref(v), _p(x), cols, _p(theirs), rows) == 1
+        else:
+            assert ref.ref_quantized_tensor_matmul_f32(ctypes.byref(v), _p(x), cols, m, _p(theirs), rows) == 1
+        ours = oracle.matvec(raw, t, rows, cols, x[0] if m == 1 else x[:m])
+        assert np.array_equal(ours.reshape(m, rows).view(np.uint32), theirs.view(np.uint32))
+
+
+def test_f16_bit_identical_to_reference(oracle):
+    ref = _ref_or_skip(oracle, "scalar")
+    r = ctypes.c_float()
+    for code in range(65536):
+        assert ref.ref_f16_bits_to_f32(code, ctypes.byref(r)) == 1
+        ours = np.float32(oracle.lib().oracle_f16_to_f32(code))
+        theirs = np.float32(r.value)
+        if math.isnan(theirs):
+            assert math.isnan(ours)
+        else:
+            assert ours.view(np.uint32) == theirs.view(np.uint32)
+
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_reference_avx2_build_within_tolerance(oracle, t):
+    """The reference's as-deployed x86 build (AVX2/FMA) reduces in another
+    order; it agrees with the scalar oracle under the row rule."""
+    ref = _ref_or_skip(oracle, "avx2")
+    be = B.BLOCK_ELEMENTS[t]
+    rows, cols = 31, 8 * be
+    raw = B.raw_blocks(t, rows * 8, seed=400 + t)
+    x = np.random.default_rng(t).standard_normal(cols).astype(np.float32)
+    v = oracle.view(raw, t, rows, cols)
+    theirs = np.empty(rows, dtype=np.float32)
+    assert ref.ref_quantized_tensor_matvec_f32(ctypes.byref(v), _p(x), cols, _p(theirs), rows) == 1
+    ours = oracle.matvec(raw, t, rows, cols, x)
+    _, absdot = oracle.row_stats(raw, t, rows, cols, x)
+    ok = np.isfinite(absdot)
+    assert np.all(np.abs(ours[ok] - theirs[ok]) <= 1e-5 * absdot[ok])
