@@ -90,13 +90,14 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
     qmv = importlib.import_module("my-inference-engine_amd")
+    hip = importlib.import_module("my-inference-engine_amd.hip_runtime")
     lib = qmv.hip_lib()
     assert lib.qmv_device_count() > 0, "no GPU"
-    torch.cuda.set_device(0)
-    stream = torch.cuda.Stream()
+    assert lib.qmv_set_device(0) == 1
+    hip.check(hip.rt().hipSetDevice(0), "hipSetDevice")
+    stream = hip.Stream()
+    sp = stream.handle
     M = args.batch
 
     # ---- weights: generated per layer on the host, uploaded, host copy dropped
@@ -116,103 +117,99 @@ def main():
         layers.append(tensors)
     upload_s = time.time() - t0
 
-    # ---- activations and outputs (per layer, resident)
-    dev = torch.device("cuda", 0)
-    gen = torch.Generator(device="cpu").manual_seed(1234)
+    # ---- activations (fp32 N(0,1), per layer) and outputs, resident in HBM
     acts, outs = [], []
     for layer in range(LAYERS):
-        a = {k: torch.randn(M, c, generator=gen).to(dev) for k, c in
-             (("attn", HIDDEN), ("o", HIDDEN), ("ffn", HIDDEN), ("down", INTER))}
-        o = {name: torch.empty(M, rows, device=dev) for name, _, rows, _ in layer_shapes()}
+        a = {k: hip.DeviceBuffer.from_array(qmv.synth_normal(M * c, seed=50000 + 10 * layer + i))
+             for i, (k, c) in enumerate((("attn", HIDDEN), ("o", HIDDEN), ("ffn", HIDDEN), ("down", INTER)))}
+        o = {name: hip.DeviceBuffer(4 * M * rows) for name, _, rows, _ in layer_shapes()}
         acts.append(a)
         outs.append(o)
-    torch.cuda.synchronize()
+    hip.synchronize()
 
-    # ---- one step = 4 launches per layer
-    launches = []  # (kernel name, algorithmic bytes, callable)
+    # ---- one step = 4 launches per layer, arguments prepared once
+    grp_fn = lib.qmv_device_matvec_group_f32
+    one_fn = lib.qmv_device_matvec_f32
+    launches = []  # (kernel name, algorithmic bytes, callable(stream))
     for layer in range(LAYERS):
         T, A, O = layers[layer], acts[layer], outs[layer]
 
         def grp(names, x, T=T, O=O):
-            ts = [T[n] for n in names]
-            ptrs = [O[n].data_ptr() for n in names]
-            return lambda s: qmv.device_matvec_group(ts, x.data_ptr(), M, ptrs, s)
+            hs = (ctypes.c_void_p * len(names))(*[T[n].handle.value for n in names])
+            ps = (ctypes.c_void_p * len(names))(*[O[n].ptr for n in names])
+            n, xp = len(names), x.ptr
+            return lambda s: grp_fn(hs, n, xp, M, ps, s)
 
         def one(name, x, T=T, O=O):
-            return lambda s: T[name].matvec(x.data_ptr(), M, O[name].data_ptr(), s)
+            h, xp, yp = T[name].handle, x.ptr, O[name].ptr
+            return lambda s: one_fn(h, xp, M, yp, s)
 
         def algo(names, cols):
             w = sum(T[n].packed_bytes for n in names)
             return w + 4 * M * cols + 4 * M * sum(T[n].rows for n in names)
 
-        launches.append(("matvec_kernel<Q4_K,%d>" % M, algo(["q", "k", "v"], HIDDEN), grp(["q", "k", "v"], A["attn"])))
-        launches.append(("matvec_kernel<Q4_K,%d>" % M, algo(["o"], HIDDEN), one("o", A["o"])))
-        launches.append(("matvec_kernel<Q4_K,%d>" % M, algo(["gate", "up"], HIDDEN), grp(["gate", "up"], A["ffn"])))
-        launches.append(("matvec_kernel<Q6_K,%d>" % M, algo(["down"], INTER), one("down", A["down"])))
+        kq, k6 = "matvec_kernel<Q4_K,%d>" % M, "matvec_kernel<Q6_K,%d>" % M
+        launches.append((kq, algo(["q", "k", "v"], HIDDEN), grp(["q", "k", "v"], A["attn"])))
+        launches.append((kq, algo(["o"], HIDDEN), one("o", A["o"])))
+        launches.append((kq, algo(["gate", "up"], HIDDEN), grp(["gate", "up"], A["ffn"])))
+        launches.append((k6, algo(["down"], INTER), one("down", A["down"])))
 
     def step(s):
         for _, _, fn in launches:
-            fn(s)
+            if fn(s) != 1:
+                raise RuntimeError(qmv.last_error())
 
-    with torch.cuda.stream(stream):
-        sp = stream.cuda_stream
-        for _ in range(max(1, args.warmup)):
-            step(sp)
-        torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup)):
+        step(sp)
+    stream.synchronize()
 
-        graph = None
-        if not args.no_graph:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                step(stream.cuda_stream)
-            for _ in range(args.warmup):
-                graph.replay()
-            torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = hip.Graph(stream)
+        graph.begin()
+        step(sp)
+        graph.end()
+        for _ in range(args.warmup):
+            graph.replay()
+        stream.synchronize()
 
-        def run_steps(k):
-            torch.cuda.synchronize()
-            t_a = time.perf_counter()
-            for _ in range(k):
-                if graph is not None:
-                    graph.replay()
-                else:
-                    step(sp)
-            torch.cuda.synchronize()
-            return time.perf_counter() - t_a
-
-        elapsed = run_steps(args.steps)
-        eager_elapsed = None
+    t_a = time.perf_counter()
+    for _ in range(args.steps):
         if graph is not None:
-            eager_elapsed = None
-            torch.cuda.synchronize()
-            t_a = time.perf_counter()
-            for _ in range(max(3, args.steps // 5)):
-                step(sp)
-            torch.cuda.synchronize()
-            eager_elapsed = (time.perf_counter() - t_a) / max(3, args.steps // 5)
+            graph.replay()
+        else:
+            step(sp)
+    stream.synchronize()
+    elapsed = time.perf_counter() - t_a
 
-        # ---- profiling pass: HIP events around every launch, same stream
-        per_kernel = {}
-        kernel_sum = []
-        for _ in range(args.profile_passes):
-            evs = []
-            for name, nbytes, fn in launches:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                fn(sp)
-                e1.record(stream)
-                evs.append((name, nbytes, e0, e1))
-            torch.cuda.synchronize()
-            tot = 0.0
-            for name, nbytes, e0, e1 in evs:
-                ms = e0.elapsed_time(e1)
-                tot += ms
-                d = per_kernel.setdefault(name, [0, 0.0, 0])
-                d[0] += nbytes
-                d[1] += ms
-                d[2] += 1
-            kernel_sum.append(tot)
+    eager_elapsed = None
+    if graph is not None:
+        reps = max(3, args.steps // 5)
+        t_a = time.perf_counter()
+        for _ in range(reps):
+            step(sp)
+        stream.synchronize()
+        eager_elapsed = (time.perf_counter() - t_a) / reps
+
+    # ---- profiling pass: HIP events around every launch, on the bench stream
+    per_kernel = {}
+    kernel_sum = []
+    evs = [(hip.Event(), hip.Event()) for _ in launches]
+    for _ in range(args.profile_passes):
+        for (name, nbytes, fn), (e0, e1) in zip(launches, evs):
+            e0.record(stream)
+            fn(sp)
+            e1.record(stream)
+        stream.synchronize()
+        tot = 0.0
+        for (name, nbytes, _), (e0, e1) in zip(launches, evs):
+            ms = e0.elapsed_ms(e1)
+            tot += ms
+            d = per_kernel.setdefault(name, [0, 0.0, 0])
+            d[0] += nbytes
+            d[1] += ms
+            d[2] += 1
+        kernel_sum.append(tot)
 
     ms_per_step = elapsed / args.steps * 1e3
     value = total_bytes / (elapsed / args.steps) / 1e9

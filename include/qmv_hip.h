@@ -162,6 +162,19 @@ int qmv_set_device(int ordinal);
 int qmv_device_count(void);
 
 /*
+ * Launch-plan tuning (process-wide; 0 keeps the automatic choice). A launch
+ * assigns each workgroup one 64-row tile and a contiguous range of K-units,
+ * processed by waves_per_group waves of units_per_wave units each; K is split
+ * across workgroups only as far as needed to reach about target_waves waves
+ * (default: half the kernel's resident-wave capacity on the device). Defaults may
+ * also come from the QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE /
+ * QMV_WAVES_PER_GROUP environment variables. Any setting stays within the row
+ * tolerance (the split of K only changes the summation order).
+ */
+void qmv_set_launch_tuning(int target_waves, int units_per_wave,
+                           int waves_per_group);
+
+/*
  * Test hook for failure propagation (the role of the reference's link-time
  * block-dot stubs, tests/quantized_matvec_failure_test.cpp:16-38): while
  * armed, the next `count` host-pointer matvec/matmul calls fail after their

@@ -20,7 +20,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-HIP_LIB_PATH = os.path.join(CSRC, "libqmv_hip.so")
+# QMV_HIP_LIB may name another build of the same library (e.g. a tuning variant).
+HIP_LIB_PATH = os.environ.get("QMV_HIP_LIB") or os.path.join(CSRC, "libqmv_hip.so")
 SYNTH_LIB_PATH = os.path.join(CSRC, "libqmv_synth.so")
 
 # GGML type codes (src/gguf_reader.h:7-11) and block geometry
@@ -101,6 +102,7 @@ HIP_SIGNATURES = {
     "qmv_set_device": (ctypes.c_int, [ctypes.c_int]),
     "qmv_device_count": (ctypes.c_int, []),
     "qmv_debug_fail_next_calls": (None, [ctypes.c_int]),
+    "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
 }
 
 SYNTH_SIGNATURES = {

@@ -38,10 +38,20 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits)
     return (float)h;
 }
 
-/* Byte k of v as a float; the backend selects the byte-select conversion. */
+/* Byte k of v as a float; the backend selects v_cvt_f32_ubyte<k>. */
 __device__ __forceinline__ float ubyte(uint32_t v, int k)
 {
     return (float)((v >> (8 * k)) & 0xffu);
+}
+
+/* v with its bit pattern hidden from the optimiser. Applied to a dword of
+ * packed codes after masking, so that each byte converts with a single
+ * v_cvt_f32_ubyte<k>: otherwise the mask is folded into every byte as a
+ * separate bit-field extract before a byte-0 conversion. */
+__device__ __forceinline__ uint32_t codes(uint32_t v)
+{
+    asm("" : "+v"(v));
+    return v;
 }
 
 __device__ __forceinline__ float sbyte(uint32_t v, int k)
@@ -236,7 +246,7 @@ __device__ __forceinline__ float q4k_m1(const Q4KUnit &u, const float *__restric
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t dw = word(u.p[1 + p], e);
-            const uint32_t lo = dw & 0x0f0f0f0fu, hi = dw & 0xf0f0f0f0u;
+            const uint32_t lo = codes(dw & 0x0f0f0f0fu), hi = codes(dw & 0xf0f0f0f0u);
             float &la = (e & 1) ? l1 : l0;
             float &ha = (e & 1) ? h1 : h0;
 #pragma unroll
@@ -272,7 +282,7 @@ __device__ __forceinline__ void q4k_w(const Q4KUnit &u, const Q4KScales &s, int 
 {
     const int g = r >> 3, h = (r >> 2) & 1, e = r & 3;
     const uint32_t dw = after(word(u.p[1 + 2 * g + h], e), dep);
-    const uint32_t lo = dw & 0x0f0f0f0fu, hi = dw & 0xf0f0f0f0u;
+    const uint32_t lo = codes(dw & 0x0f0f0f0fu), hi = codes(dw & 0xf0f0f0f0u);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         /* a*q is exact, so the fused form rounds exactly like a*q - m. */
@@ -288,10 +298,10 @@ __device__ __forceinline__ void q4k_w(const Q4KUnit &u, const Q4KScales &s, int 
  * 8+2g+oh; dword e covers o = 16oh + 4e .. +3. */
 __device__ __forceinline__ void q6k_codes(uint32_t qa, uint32_t qb, uint32_t qh, uint32_t (&q)[4])
 {
-    q[0] = (qa & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u);
-    q[1] = (qb & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u);
-    q[2] = ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u);
-    q[3] = ((qb >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u);
+    q[0] = codes((qa & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u));
+    q[1] = codes((qb & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u));
+    q[2] = codes(((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u));
+    q[3] = codes(((qb >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u));
 }
 
 __device__ __forceinline__ void q6k_dscales(const Q6KUnit &u, float (&dsc)[16])
@@ -344,6 +354,8 @@ __device__ __forceinline__ float q6k_m1(const Q6KUnit &u, const float *__restric
                 q0 = ((word(u.p[4 * g + oh], e) >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u);
                 q1 = ((word(u.p[4 * g + 2 + oh], e) >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u);
             }
+            q0 = codes(q0);
+            q1 = codes(q1);
             float &a0 = (e & 1) ? c01 : c00;
             float &a1 = (e & 1) ? c11 : c10;
 #pragma unroll
@@ -424,7 +436,7 @@ __device__ __forceinline__ float q80_m1(const Q80Unit &u, const float *__restric
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t dw = word(u.qs[2 * j + h], e) ^ 0x80808080u;
+                    const uint32_t dw = codes(word(u.qs[2 * j + h], e) ^ 0x80808080u);
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc)
                         c[2 * h + (e & 1)] = fmaf(ubyte(dw, cc), x[16 * h + 4 * e + cc], c[2 * h + (e & 1)]);
@@ -447,7 +459,7 @@ __device__ __forceinline__ void q80_w(const Q80Unit &u, const float (&d)[4], int
     const int j = r >> 2, h = (r >> 1) & 1, ep = r & 1;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint32_t dw = after(word(u.qs[2 * j + h], 2 * ep + (i >> 2)), dep) ^ 0x80808080u;
+        const uint32_t dw = codes(after(word(u.qs[2 * j + h], 2 * ep + (i >> 2)), dep) ^ 0x80808080u);
         if (kSignedZeros) w[i] = d[j] * (ubyte(dw, i & 3) - 128.0f);
         else w[i] = fmaf(d[j], ubyte(dw, i & 3), -128.0f * d[j]); /* d*(q+128) - 128d == d*q */
     }
@@ -458,8 +470,8 @@ __device__ __forceinline__ void q80_w(const Q80Unit &u, const float (&d)[4], int
  * nib | bit << 4 in 0..31, value d * (q - 16). */
 __device__ __forceinline__ void q50_codes(uint32_t dw, uint32_t qh, int e, uint32_t &lo, uint32_t &hi)
 {
-    lo = (dw & 0x0f0f0f0fu) | spread_bits4((qh >> (4 * e)) & 15u);
-    hi = ((dw >> 4) & 0x0f0f0f0fu) | spread_bits4((qh >> (16 + 4 * e)) & 15u);
+    lo = codes((dw & 0x0f0f0f0fu) | spread_bits4((qh >> (4 * e)) & 15u));
+    hi = codes(((dw >> 4) & 0x0f0f0f0fu) | spread_bits4((qh >> (16 + 4 * e)) & 15u));
 }
 
 __device__ __forceinline__ float q50_d(const Q50Unit &u, int j)
@@ -650,10 +662,28 @@ __device__ __forceinline__ void unit_step(const typename UnitOf<FMT>::T &u, cons
     }
 }
 
-/* ---- matvec kernel --------------------------------------------------------- */
+/* ---- matvec kernel ---------------------------------------------------------
+ * Workgroup = one 64-row tile x one K-split; its waves take consecutive
+ * K-units and combine through LDS in wave order. A tile whose K is split
+ * across workgroups is finished by the last split to arrive, which adds the
+ * published partials in split order. */
+
+/* Minimum resident waves per SIMD the matvec kernels are compiled for (caps
+ * VGPRs at 512 / n; 1 leaves register allocation to the compiler);
+ * QMV_WAVES_PER_SIMD_M1 / _MN are build-time knobs. */
+#ifndef QMV_WAVES_PER_SIMD_M1
+#define QMV_WAVES_PER_SIMD_M1 1
+#endif
+#ifndef QMV_WAVES_PER_SIMD_MN
+#define QMV_WAVES_PER_SIMD_MN 1
+#endif
+template <int FMT, int M> struct MatvecOccupancy {
+    static constexpr int value = M == 1 ? QMV_WAVES_PER_SIMD_M1 : QMV_WAVES_PER_SIMD_MN;
+};
 
 template <int FMT, int M>
 __global__ void __launch_bounds__(QMV_MAX_WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(MatvecOccupancy<FMT, M>::value)))
 matvec_kernel(MatvecParams p)
 {
     using Unit = typename UnitOf<FMT>::T;
@@ -719,26 +749,34 @@ matvec_kernel(MatvecParams p)
     }
 
     /* Split K: publish this split's partial, the last split to arrive adds
-     * all partials of the tile in split order. */
+     * all partials of the tile in split order (a fixed order, so results do
+     * not depend on arrival order). Partials and counters are accessed only
+     * with agent-scope atomics, which are coherent across the XCDs' L2s
+     * without a cache writeback or invalidate: the wait for the partial
+     * stores to complete orders them before the arrival count. */
     float *part = p.partials + job.partial_offset + ((size_t)tile * job.splits) * M * 64;
+    unsigned *count = p.counters + job.counter_offset + tile;
 #pragma unroll
-    for (int m = 0; m < M; ++m) part[((size_t)split * M + m) * 64 + lane] = sum[m];
-    __threadfence(); /* release: the partials are visible device-wide */
+    for (int m = 0; m < M; ++m)
+        __hip_atomic_store(part + ((size_t)split * M + m) * 64 + lane, sum[m], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned prev = 0;
-    if (lane == 0) prev = atomicAdd(p.counters + job.counter_offset + tile, 1u);
-    prev = __builtin_amdgcn_readlane(prev, 0);
+    if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
     if (prev != (unsigned)job.splits - 1u) return;
-    __threadfence(); /* acquire: see every other split's partials */
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         float s = 0.0f;
         for (int sp = 0; sp < job.splits; ++sp) {
-            const float v = part[((size_t)sp * M + m) * 64 + lane];
+            const float v = __hip_atomic_load(part + ((size_t)sp * M + m) * 64 + lane, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
             s = sp == 0 ? v : s + v;
         }
         if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
     }
-    if (lane == 0) p.counters[job.counter_offset + tile] = 0u;
+    if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------
@@ -887,31 +925,53 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
     return hipGetLastError();
 }
 
-template <int FMT>
-static hipError_t launch_matvec_f(const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
+template <int FMT, int M>
+static int waves_per_cu_fm()
 {
-    switch (m) {
-    case 1: return launch_matvec_fm<FMT, 1>(p, grid, waves, s);
-    case 2: return launch_matvec_fm<FMT, 2>(p, grid, waves, s);
-    case 3: return launch_matvec_fm<FMT, 3>(p, grid, waves, s);
-    case 4: return launch_matvec_fm<FMT, 4>(p, grid, waves, s);
-    case 5: return launch_matvec_fm<FMT, 5>(p, grid, waves, s);
-    case 6: return launch_matvec_fm<FMT, 6>(p, grid, waves, s);
-    case 7: return launch_matvec_fm<FMT, 7>(p, grid, waves, s);
-    case 8: return launch_matvec_fm<FMT, 8>(p, grid, waves, s);
-    default: return hipErrorInvalidValue;
-    }
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, matvec_kernel<FMT, M>, 64, 0) != hipSuccess)
+        return 0;
+    return blocks; /* one-wave workgroups: blocks == waves */
 }
+
+#define QMV_FOR_M(MACRO, FMT)                                                                          \
+    switch (m) {                                                                                       \
+    case 1: return MACRO(FMT, 1);                                                                      \
+    case 2: return MACRO(FMT, 2);                                                                      \
+    case 3: return MACRO(FMT, 3);                                                                      \
+    case 4: return MACRO(FMT, 4);                                                                      \
+    case 5: return MACRO(FMT, 5);                                                                      \
+    case 6: return MACRO(FMT, 6);                                                                      \
+    case 7: return MACRO(FMT, 7);                                                                      \
+    case 8: return MACRO(FMT, 8);                                                                      \
+    default: break;                                                                                    \
+    }
+
+#define QMV_LAUNCH(FMT, M) launch_matvec_fm<FMT, M>(p, grid, waves, s)
+#define QMV_OCC(FMT, M) waves_per_cu_fm<FMT, M>()
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
 {
     switch (fmt) {
-    case QMV_FMT_Q4_K: return launch_matvec_f<QMV_FMT_Q4_K>(p, m, grid, waves, s);
-    case QMV_FMT_Q6_K: return launch_matvec_f<QMV_FMT_Q6_K>(p, m, grid, waves, s);
-    case QMV_FMT_Q8_0: return launch_matvec_f<QMV_FMT_Q8_0>(p, m, grid, waves, s);
-    case QMV_FMT_Q5_0: return launch_matvec_f<QMV_FMT_Q5_0>(p, m, grid, waves, s);
-    default: return hipErrorInvalidValue;
+    case QMV_FMT_Q4_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K) break;
+    case QMV_FMT_Q6_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K) break;
+    case QMV_FMT_Q8_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q8_0) break;
+    case QMV_FMT_Q5_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q5_0) break;
+    default: break;
     }
+    return hipErrorInvalidValue;
+}
+
+int matvec_waves_per_cu(int fmt, int m)
+{
+    switch (fmt) {
+    case QMV_FMT_Q4_K: QMV_FOR_M(QMV_OCC, QMV_FMT_Q4_K) break;
+    case QMV_FMT_Q6_K: QMV_FOR_M(QMV_OCC, QMV_FMT_Q6_K) break;
+    case QMV_FMT_Q8_0: QMV_FOR_M(QMV_OCC, QMV_FMT_Q8_0) break;
+    case QMV_FMT_Q5_0: QMV_FOR_M(QMV_OCC, QMV_FMT_Q5_0) break;
+    default: break;
+    }
+    return 0;
 }
 
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,

@@ -377,29 +377,54 @@ int env_int(const char *name, int dflt)
     return atoi(v);
 }
 
+std::atomic<int> g_target_waves{env_int("QMV_TARGET_WAVES", 0)};
+std::atomic<int> g_force_u{env_int("QMV_UNITS_PER_WAVE", 0)};
+std::atomic<int> g_force_w{env_int("QMV_WAVES_PER_GROUP", 0)};
+
+/* Resident-wave capacity of the device for one kernel (fmt, M), cached. */
+int resident_waves(int device, int fmt, int m)
+{
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    auto key = std::make_tuple(device, fmt, m);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+        cus = 256;
+    int per_cu = qmv::matvec_waves_per_cu(fmt, m);
+    if (per_cu <= 0) per_cu = 8;
+    const int waves = cus * per_cu;
+    cache[key] = waves;
+    return waves;
+}
+
 struct Plan {
     int units_per_wave, waves, splits, units_per_split;
 };
 
-/* Spread tiles x units over waves: aim for ~8 resident waves per CU across
- * 256 CUs, at most 8 waves per workgroup, and split K across workgroups only
- * as far as needed to fill the GPU. QMV_UNITS_PER_WAVE / QMV_WAVES override. */
-Plan plan_for(long long total_tiles, int units)
+/* Spread tiles x K-units over waves so that about `target` waves (half a
+ * resident round of the kernel unless tuned) share the work, with at most QMV_MAX_WAVES
+ * waves per workgroup along K, and split K across workgroups only as far as
+ * the wave count needs. */
+Plan plan_for(long long total_tiles, int units, int device, int fmt, int m)
 {
-    static const int target = env_int("QMV_TARGET_WAVES", 2048);
-    static const int force_u = env_int("QMV_UNITS_PER_WAVE", 0);
-    static const int force_w = env_int("QMV_WAVES", 0);
+    int target = g_target_waves.load();
+    if (target <= 0) target = resident_waves(device, fmt, m) / 2;
+    const int force_u = g_force_u.load();
+    const int force_w = g_force_w.load();
     const long long work = total_tiles * (long long)units;
-    int U = (int)((work + target - 1) / target);
-    U = U < 1 ? 1 : U > 8 ? 8 : U;
+    long long u = (work + target - 1) / target;
+    int U = (int)(u < 1 ? 1 : u > 8 ? 8 : u);
     if (force_u > 0) U = force_u;
     if (U > units) U = units;
     int W = (units + U - 1) / U;
     W = W < 1 ? 1 : W > QMV_MAX_WAVES ? QMV_MAX_WAVES : W;
-    if (force_w > 0 && force_w <= QMV_MAX_WAVES) W = force_w;
+    if (force_w > 0) W = force_w;
     int S = (units + W * U - 1) / (W * U);
-    /* Rebalance so the splits are even. */
-    int ups = (units + S - 1) / S;
+    /* Even splits: every split gets ceil(units / S) units. */
+    const int ups = (units + S - 1) / S;
     if (force_u <= 0) U = (ups + W - 1) / W;
     if (force_w <= 0) W = (ups + U - 1) / U;
     S = (units + ups - 1) / ups;
@@ -418,7 +443,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const QmvDeviceTensor *t0 = ts[0];
     long long total_tiles = 0;
     for (int i = 0; i < count; ++i) total_tiles += ts[i]->tiles;
-    const Plan plan = plan_for(total_tiles, t0->units);
+    const Plan plan = plan_for(total_tiles, t0->units, t0->device, t0->geo.format, batch);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
@@ -721,6 +746,13 @@ QMV_API int qmv_device_count(void)
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
     return n;
+}
+
+QMV_API void qmv_set_launch_tuning(int target_waves, int units_per_wave, int waves_per_group)
+{
+    g_target_waves.store(target_waves > 0 ? target_waves : 0);
+    g_force_u.store(units_per_wave > 0 ? units_per_wave : 0);
+    g_force_w.store(waves_per_group > 0 && waves_per_group <= QMV_MAX_WAVES ? waves_per_group : 0);
 }
 
 QMV_API void qmv_debug_fail_next_calls(int count)

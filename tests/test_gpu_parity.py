@@ -344,58 +344,90 @@ def test_cache_follows_new_contents(qmv, gpu):
     qmv.release_all()
 
 
-def test_device_api_matches_host_api(qmv, gpu):
-    torch = pytest.importorskip("torch")
+@pytest.fixture(scope="module")
+def hip(qmv):
+    import importlib
+    return importlib.import_module("my-inference-engine_amd.hip_runtime")
+
+
+def test_device_api_matches_host_api(qmv, gpu, hip):
     t, rows, cols = B.Q4_K, 18944, 3584
     raw = qmv.synth_tensor(t, rows, cols, seed=21)
     v = qmv.make_view(raw, t, rows, cols)
     dt = qmv.DeviceTensor(v)
     assert (dt.rows, dt.cols, dt.packed_bytes) == (rows, cols, raw.size)
     x = qmv.synth_normal(8 * cols, seed=22).reshape(8, cols)
-    dx = torch.from_numpy(x).cuda()
-    dy = torch.empty((8, rows), device="cuda", dtype=torch.float32)
-    stream = torch.cuda.current_stream().cuda_stream
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(8 * rows * 4)
+    stream = hip.Stream()
     for m in (1, 8):
-        dt.matvec(dx.data_ptr(), m, dy.data_ptr(), stream)
-        torch.cuda.synchronize()
+        dt.matvec(dx.ptr, m, dy.ptr, stream.handle)
+        stream.synchronize()
         host = qmv.matvec(v, x[:m] if m > 1 else x[0]).reshape(m, rows)
-        assert np.array_equal(dy[:m].cpu().numpy().view(np.uint32), host.view(np.uint32))
-    # device dequant equals host dequant
-    out = torch.empty((5, cols), device="cuda", dtype=torch.float32)
-    dt.dequantize(100, 5, out.data_ptr(), stream)
-    torch.cuda.synchronize()
-    assert np.array_equal(out.cpu().numpy().view(np.uint32), qmv.dequantize_rows(v, 100, 5).view(np.uint32))
+        got = dy.to_array(np.float32, (8, rows))[:m]
+        assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
+    out = hip.DeviceBuffer(5 * cols * 4)
+    dt.dequantize(100, 5, out.ptr, stream.handle)
+    stream.synchronize()
+    assert np.array_equal(out.to_array(np.float32, (5, cols)).view(np.uint32),
+                          qmv.dequantize_rows(v, 100, 5).view(np.uint32))
     dt.close()
     qmv.release_all()
 
 
-def test_group_launch_matches_single(qmv, oracle, gpu):
+def test_group_launch_matches_oracle(qmv, oracle, gpu, hip):
     """q/k/v sharing one input in one launch: each within tolerance of the oracle."""
-    torch = pytest.importorskip("torch")
     cols = 3584
     shapes = [(3584, 31), (512, 32), (512, 33)]
     raws = [qmv.synth_tensor(B.Q4_K, r, cols, seed=s) for r, s in shapes]
     dts = [qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, r, cols)) for raw, (r, _) in zip(raws, shapes)]
     x = qmv.synth_normal(cols, seed=34)
-    dx = torch.from_numpy(x).cuda()
-    outs = [torch.empty(r, device="cuda", dtype=torch.float32) for r, _ in shapes]
-    qmv.device_matvec_group(dts, dx.data_ptr(), 1, [o.data_ptr() for o in outs],
-                            torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
+    dx = hip.DeviceBuffer.from_array(x)
+    outs = [hip.DeviceBuffer(4 * r) for r, _ in shapes]
+    stream = hip.Stream()
+    qmv.device_matvec_group(dts, dx.ptr, 1, [o.ptr for o in outs], stream.handle)
+    stream.synchronize()
     for raw, (r, _), o in zip(raws, shapes, outs):
         y_ref = oracle.matvec(raw, B.Q4_K, r, cols, x)
         _, absdot = oracle.row_stats(raw, B.Q4_K, r, cols, x)
-        check_rows(o.cpu().numpy(), y_ref, absdot, "group")
+        check_rows(o.to_array(np.float32, (r,)), y_ref, absdot, "group")
     for d in dts:
         d.close()
 
 
-def test_device_argmax(qmv, gpu):
-    torch = pytest.importorskip("torch")
+def test_graph_replays_match_eager(qmv, gpu, hip):
+    """A captured launch (split-K counters reset by the kernel itself, no
+    memset nodes) replays to the eager result, with host work in between."""
+    t, rows, cols = B.Q6_K, 3584, 18944
+    raw = qmv.synth_tensor(t, rows, cols, seed=61)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+    x = qmv.synth_normal(cols, seed=62)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(4 * rows)
+    stream = hip.Stream()
+    dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)  # sizes the stream's workspace
+    stream.synchronize()
+    eager = dy.to_array(np.float32, (rows,))
+    g = hip.Graph(stream)
+    g.begin()
+    dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)
+    g.end()
+    for i in range(5):
+        dy.fill(0)
+        g.replay()
+        stream.synchronize()
+        assert np.array_equal(dy.to_array(np.float32, (rows,)).view(np.uint32), eager.view(np.uint32)), i
+        dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)  # eager work between replays
+        stream.synchronize()
+    dt.close()
+
+
+def test_device_argmax(qmv, gpu, hip):
     x = np.random.default_rng(5).standard_normal(151936).astype(np.float32)
     x[[10, 150000]] = 9.0
-    dx = torch.from_numpy(x).cuda()
-    res = torch.full((2,), -5, device="cuda", dtype=torch.int32)
-    qmv.device_greedy_argmax(dx.data_ptr(), x.size, res.data_ptr(), torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-    assert res.cpu().tolist() == [10, 1]
+    dx = hip.DeviceBuffer.from_array(x)
+    res = hip.DeviceBuffer(8)
+    stream = hip.Stream()
+    qmv.device_greedy_argmax(dx.ptr, x.size, res.ptr, stream.handle)
+    stream.synchronize()
+    assert res.to_array(np.int32, (2,)).tolist() == [10, 1]
