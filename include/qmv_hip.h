@@ -162,14 +162,18 @@ int qmv_set_device(int ordinal);
 int qmv_device_count(void);
 
 /*
- * Launch-plan tuning (process-wide; 0 keeps the automatic choice). A launch
- * assigns each workgroup one 64-row tile and a contiguous range of K-units,
- * processed by waves_per_group waves of units_per_wave units each; K is split
- * across workgroups only as far as needed to reach about target_waves waves
- * (default: half the kernel's resident-wave capacity on the device). Defaults may
- * also come from the QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE /
- * QMV_WAVES_PER_GROUP environment variables. Any setting stays within the row
- * tolerance (the split of K only changes the summation order).
+ * Launch-plan tuning (process-wide; 0 keeps the automatic choice for any
+ * argument). A launch gives each workgroup one 64-row tile and a contiguous
+ * range of K-units, processed by waves_per_group waves of units_per_wave
+ * units each (default: 1 unit, 4 waves, or 8 for rows of 32 or more
+ * K-units); a tile's K is split across
+ * workgroups as far as that requires, and the last split to finish adds the
+ * partials in split order. target_waves, if set, instead grows the units per
+ * wave until about that many waves cover the launch. Defaults may also come
+ * from the QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP
+ * environment variables. Any setting stays within the row tolerance: the plan
+ * only changes the summation order, and a given plan always sums in the same
+ * order.
  */
 void qmv_set_launch_tuning(int target_waves, int units_per_wave,
                            int waves_per_group);

@@ -203,6 +203,11 @@ def greedy_sample(logits: np.ndarray):
     return ok, tok.value
 
 
+def set_launch_tuning(target_waves: int = 0, units_per_wave: int = 0, waves_per_group: int = 0) -> None:
+    """Process-wide launch-plan override (0 = automatic); see qmv_hip.h."""
+    hip_lib().qmv_set_launch_tuning(target_waves, units_per_wave, waves_per_group)
+
+
 def register_tensor(view: QmvTensorView) -> int:
     return hip_lib().qmv_register_tensor(ctypes.byref(view))
 

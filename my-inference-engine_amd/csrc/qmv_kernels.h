@@ -41,8 +41,6 @@ struct MatvecParams {
 };
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
-/* Resident waves per CU of matvec_kernel<fmt, m> (0 if unknown). */
-int matvec_waves_per_cu(int fmt, int m);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,

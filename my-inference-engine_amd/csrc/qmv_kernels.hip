@@ -124,11 +124,14 @@ __device__ __forceinline__ uint32_t word(const uint4 &v, int e)
 }
 __device__ __forceinline__ uint32_t word(const uint2 &v, int e) { return e == 0 ? v.x : v.y; }
 
-/* Activations are read through global-address-space pointers (so uniform
- * reads become scalar loads). kGuard marks the partial last unit of a
- * Q8_0/Q5_0 row: K is a multiple of 32, so it only lacks whole blocks, whose
- * regions are skipped. */
-typedef const float __attribute__((address_space(1))) gfloat;
+/* Activations are read through constant-address-space pointers: the
+ * activations are read-only while a kernel runs, and the constant space lets
+ * uniform reads be scalar loads even where the kernel also stores to global
+ * memory (a global-space read is kept scalar only when no store of the
+ * kernel could reach it). kGuard marks the partial last unit of a Q8_0/Q5_0
+ * row: K is a multiple of 32, so it only lacks whole blocks, whose regions
+ * are skipped. */
+typedef const float __attribute__((address_space(4))) gfloat;
 
 /* Activation loads are ordered by data dependencies alone. The pointer of
  * region p+1 is passed through an empty asm that also consumes one
@@ -137,7 +140,7 @@ typedef const float __attribute__((address_space(1))) gfloat;
  * issued, region p-1's FMAs are done (its activations dead) before that, and
  * no optimiser can merge, hoist or sink work across regions: at most two
  * regions of activations are live in SGPRs. The result is still a uniform
- * global pointer, so the loads stay scalar. */
+ * constant-space pointer, so the loads stay scalar. */
 __device__ __forceinline__ gfloat *region_ptr(const float *p, float dep_s, float dep_v0, float dep_v1)
 {
     gfloat *g = (gfloat *)p;
@@ -662,6 +665,33 @@ __device__ __forceinline__ void unit_step(const typename UnitOf<FMT>::T &u, cons
     }
 }
 
+/* Coherent (agent-scope) loads and stores of published partials. */
+__device__ __forceinline__ float load_partial(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_partial(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Sum of the n partials part[i * stride] (i = 0..n-1, this lane's element),
+ * added in index order. Loads go out in batches of 16 before any is waited
+ * for, so a sum costs ceil(n / 16) memory round trips. */
+__device__ __forceinline__ float sum_partials(const float *part, size_t stride, int n)
+{
+    float s = 0.0f;
+    for (int b = 0; b < n; b += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = b + i < n ? load_partial(part + (size_t)(b + i) * stride) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (b + i < n) s = b + i == 0 ? v[i] : s + v[i];
+    }
+    return s;
+}
+
 /* ---- matvec kernel ---------------------------------------------------------
  * Workgroup = one 64-row tile x one K-split; its waves take consecutive
  * K-units and combine through LDS in wave order. A tile whose K is split
@@ -681,7 +711,9 @@ template <int FMT, int M> struct MatvecOccupancy {
     static constexpr int value = M == 1 ? QMV_WAVES_PER_SIMD_M1 : QMV_WAVES_PER_SIMD_MN;
 };
 
-template <int FMT, int M>
+/* kOne: every wave takes at most one unit (units_per_wave == 1), so no
+ * second unit buffer is live and more waves fit per SIMD. */
+template <int FMT, int M, bool kOne>
 __global__ void __launch_bounds__(QMV_MAX_WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(MatvecOccupancy<FMT, M>::value)))
 matvec_kernel(MatvecParams p)
@@ -711,7 +743,13 @@ matvec_kernel(MatvecParams p)
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
-    if (u_begin < u_end) {
+    if (kOne) {
+        if (u_begin < u_end) {
+            Unit a;
+            load_unit(a, wtile + (size_t)u_begin * SLAB, lane);
+            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u_begin, lane, acc);
+        }
+    } else if (u_begin < u_end) {
         /* Two units in flight per wave: the next unit's planes are loading
          * while the current one is decoded. */
         Unit a, b;
@@ -757,9 +795,7 @@ matvec_kernel(MatvecParams p)
     float *part = p.partials + job.partial_offset + ((size_t)tile * job.splits) * M * 64;
     unsigned *count = p.counters + job.counter_offset + tile;
 #pragma unroll
-    for (int m = 0; m < M; ++m)
-        __hip_atomic_store(part + ((size_t)split * M + m) * 64 + lane, sum[m], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    for (int m = 0; m < M; ++m) store_partial(part + ((size_t)split * M + m) * 64 + lane, sum[m]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned prev = 0;
     if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -768,12 +804,7 @@ matvec_kernel(MatvecParams p)
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        float s = 0.0f;
-        for (int sp = 0; sp < job.splits; ++sp) {
-            const float v = __hip_atomic_load(part + ((size_t)sp * M + m) * 64 + lane, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-            s = sp == 0 ? v : s + v;
-        }
+        const float s = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
         if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
     }
     if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -921,17 +952,11 @@ argmax_stage2(const float *__restrict__ bval, const int *__restrict__ bidx, cons
 template <int FMT, int M>
 static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
 {
-    hipLaunchKernelGGL((matvec_kernel<FMT, M>), dim3(grid), dim3(waves * 64), 0, s, p);
+    if (p.units_per_wave == 1)
+        hipLaunchKernelGGL((matvec_kernel<FMT, M, true>), dim3(grid), dim3(waves * 64), 0, s, p);
+    else
+        hipLaunchKernelGGL((matvec_kernel<FMT, M, false>), dim3(grid), dim3(waves * 64), 0, s, p);
     return hipGetLastError();
-}
-
-template <int FMT, int M>
-static int waves_per_cu_fm()
-{
-    int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, matvec_kernel<FMT, M>, 64, 0) != hipSuccess)
-        return 0;
-    return blocks; /* one-wave workgroups: blocks == waves */
 }
 
 #define QMV_FOR_M(MACRO, FMT)                                                                          \
@@ -948,7 +973,6 @@ static int waves_per_cu_fm()
     }
 
 #define QMV_LAUNCH(FMT, M) launch_matvec_fm<FMT, M>(p, grid, waves, s)
-#define QMV_OCC(FMT, M) waves_per_cu_fm<FMT, M>()
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
 {
@@ -960,18 +984,6 @@ hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int wa
     default: break;
     }
     return hipErrorInvalidValue;
-}
-
-int matvec_waves_per_cu(int fmt, int m)
-{
-    switch (fmt) {
-    case QMV_FMT_Q4_K: QMV_FOR_M(QMV_OCC, QMV_FMT_Q4_K) break;
-    case QMV_FMT_Q6_K: QMV_FOR_M(QMV_OCC, QMV_FMT_Q6_K) break;
-    case QMV_FMT_Q8_0: QMV_FOR_M(QMV_OCC, QMV_FMT_Q8_0) break;
-    case QMV_FMT_Q5_0: QMV_FOR_M(QMV_OCC, QMV_FMT_Q5_0) break;
-    default: break;
-    }
-    return 0;
 }
 
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,

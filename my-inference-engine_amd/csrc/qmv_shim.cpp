@@ -381,47 +381,32 @@ std::atomic<int> g_target_waves{env_int("QMV_TARGET_WAVES", 0)};
 std::atomic<int> g_force_u{env_int("QMV_UNITS_PER_WAVE", 0)};
 std::atomic<int> g_force_w{env_int("QMV_WAVES_PER_GROUP", 0)};
 
-/* Resident-wave capacity of the device for one kernel (fmt, M), cached. */
-int resident_waves(int device, int fmt, int m)
-{
-    static std::mutex mu;
-    static std::map<std::tuple<int, int, int>, int> cache;
-    std::lock_guard<std::mutex> lock(mu);
-    auto key = std::make_tuple(device, fmt, m);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
-        cus = 256;
-    int per_cu = qmv::matvec_waves_per_cu(fmt, m);
-    if (per_cu <= 0) per_cu = 8;
-    const int waves = cus * per_cu;
-    cache[key] = waves;
-    return waves;
-}
-
 struct Plan {
     int units_per_wave, waves, splits, units_per_split;
 };
 
-/* Spread tiles x K-units over waves so that about `target` waves (half a
- * resident round of the kernel unless tuned) share the work, with at most QMV_MAX_WAVES
- * waves per workgroup along K, and split K across workgroups only as far as
- * the wave count needs. */
-Plan plan_for(long long total_tiles, int units, int device, int fmt, int m)
+/* Default: one K-unit per wave, four waves per workgroup (one per SIMD), or
+ * eight for long rows (>= 32 K-units), where fewer splits per tile means
+ * fewer partials for the last split to add. Many short workgroups keep every
+ * CU streaming until the end and let the dispatcher balance the load; on
+ * MI355X this beat longer waves and stream-K partitions at every decode shape
+ * measured. With target_waves set, units per wave grow instead until about
+ * that many waves cover the launch. */
+Plan plan_for(long long total_tiles, int units)
 {
-    int target = g_target_waves.load();
-    if (target <= 0) target = resident_waves(device, fmt, m) / 2;
+    const int target = g_target_waves.load();
     const int force_u = g_force_u.load();
     const int force_w = g_force_w.load();
-    const long long work = total_tiles * (long long)units;
-    long long u = (work + target - 1) / target;
-    int U = (int)(u < 1 ? 1 : u > 8 ? 8 : u);
+    int U = 1;
+    if (target > 0) {
+        const long long u = (total_tiles * (long long)units + target - 1) / target;
+        U = (int)(u < 1 ? 1 : u > 8 ? 8 : u);
+    }
     if (force_u > 0) U = force_u;
     if (U > units) U = units;
-    int W = (units + U - 1) / U;
-    W = W < 1 ? 1 : W > QMV_MAX_WAVES ? QMV_MAX_WAVES : W;
-    if (force_w > 0) W = force_w;
+    int W = force_w > 0 ? force_w : target > 0 || units >= 32 ? QMV_MAX_WAVES : 4;
+    const int need = (units + U - 1) / U;
+    if (W > need) W = need;
     int S = (units + W * U - 1) / (W * U);
     /* Even splits: every split gets ceil(units / S) units. */
     const int ups = (units + S - 1) / S;
@@ -443,7 +428,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const QmvDeviceTensor *t0 = ts[0];
     long long total_tiles = 0;
     for (int i = 0; i < count; ++i) total_tiles += ts[i]->tiles;
-    const Plan plan = plan_for(total_tiles, t0->units, t0->device, t0->geo.format, batch);
+    const Plan plan = plan_for(total_tiles, t0->units);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);

@@ -257,6 +257,27 @@ def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
     matvec_parity(qmv, oracle, t, rows, cols, seed=rows + cols, what="odd shape")
 
 
+# Launch plans: (target_waves, units_per_wave, waves_per_group). The default
+# gives every wave one unit (the single-unit kernel variant); the others run
+# the two-unit pipelined variant, one wave per workgroup, whole-K workgroups
+# (no split) and target-sized units.
+PLANS = [(0, 0, 0), (0, 2, 0), (0, 3, 7), (0, 1, 1), (0, 1, 8), (2048, 0, 0), (0, 2, 1), (0, 8, 8), (0, 5, 3)]
+
+
+@pytest.mark.parametrize("plan", PLANS)
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_launch_plans_match_oracle(qmv, oracle, gpu, plan, t):
+    """Every plan stays within tolerance, including a partial last unit
+    (Q8_0/Q5_0 with K = 7 blocks of 32) and batches of 3 and 8."""
+    cols = 5 * B.BLOCK_ELEMENTS[t] if t in (B.Q4_K, B.Q6_K) else 7 * 32 + 512
+    qmv.set_launch_tuning(*plan)
+    try:
+        for batch in (1, 3, 8):
+            matvec_parity(qmv, oracle, t, 130, cols, batch=batch, seed=batch + 40, what=f"plan {plan}")
+    finally:
+        qmv.set_launch_tuning(0, 0, 0)
+
+
 def test_config4_vocab_projection_and_argmax(qmv, oracle, gpu):
     """Q6_K 151936 x 3584 (446 MB) then greedy argmax: the index equals the
     CPU argmax of the oracle's logits."""
