@@ -9,9 +9,15 @@ launches, the grouping a real decode step's data dependencies allow:
 112 launches of a step are captured once in a HIP graph and replayed.
 
 Prints one JSON line: value = packed weight bytes / wall time per step
-(GB/s), the roofline of the dominant kernel (HIP events around each launch
-of a separate profiling pass over the same resident weights), and the CPU
-baseline (the reference's own x86 build, AVX2 + OpenMP, on a bounded sample).
+(GB/s) over the timed graph replays, the roofline of the dominant kernel
+(its launches of one step captured in a graph of their own and replayed
+between two HIP events on the stream the kernels run on, over the same
+resident weights), the HBM traffic per
+launch from the committed rocprofv3 counter summary when it covers this
+kernel and workload, and the CPU baseline (the reference's own x86 build,
+AVX2 + OpenMP, on a bounded sample). `extra` adds the same set at M=8, the
+per-step p10/p50/p90, eager (ungraphed) launch time and a measured streaming
+read bandwidth.
 """
 import argparse
 import ctypes
@@ -74,60 +80,8 @@ def cpu_baseline(qmv, host_layer, batch, seconds):
                       f"OMP_NUM_THREADS={threads})"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=1, help="positions per matvec (1 = decode, <= 8)")
-    ap.add_argument("--profile-passes", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this path has no multi-GPU mode); got --gpus {args.gpus}",
-              file=sys.stderr)
-        sys.exit(2)
-
-    qmv = importlib.import_module("my-inference-engine_amd")
-    hip = importlib.import_module("my-inference-engine_amd.hip_runtime")
-    lib = qmv.hip_lib()
-    assert lib.qmv_device_count() > 0, "no GPU"
-    assert lib.qmv_set_device(0) == 1
-    hip.check(hip.rt().hipSetDevice(0), "hipSetDevice")
-    stream = hip.Stream()
-    sp = stream.handle
-    M = args.batch
-
-    # ---- weights: generated per layer on the host, uploaded, host copy dropped
-    t0 = time.time()
-    layers, host_layer0, total_bytes = [], None, 0
-    for layer in range(LAYERS):
-        tensors = {}
-        keep = []
-        for j, (name, t, rows, cols) in enumerate(layer_shapes()):
-            raw = qmv.synth_tensor(t, rows, cols, seed=1000 * layer + j)
-            total_bytes += raw.size
-            tensors[name] = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
-            if layer == 0:
-                keep.append((name, t, rows, cols, raw))
-        if layer == 0:
-            host_layer0 = keep
-        layers.append(tensors)
-    upload_s = time.time() - t0
-
-    # ---- activations (fp32 N(0,1), per layer) and outputs, resident in HBM
-    acts, outs = [], []
-    for layer in range(LAYERS):
-        a = {k: hip.DeviceBuffer.from_array(qmv.synth_normal(M * c, seed=50000 + 10 * layer + i))
-             for i, (k, c) in enumerate((("attn", HIDDEN), ("o", HIDDEN), ("ffn", HIDDEN), ("down", INTER)))}
-        o = {name: hip.DeviceBuffer(4 * M * rows) for name, _, rows, _ in layer_shapes()}
-        acts.append(a)
-        outs.append(o)
-    hip.synchronize()
-
-    # ---- one step = 4 launches per layer, arguments prepared once
+def build_launches(lib, layers, acts, outs, M):
+    """One step = 4 launches per layer, arguments prepared once."""
     grp_fn = lib.qmv_device_matvec_group_f32
     one_fn = lib.qmv_device_matvec_f32
     launches = []  # (kernel name, algorithmic bytes, callable(stream))
@@ -153,72 +107,206 @@ def main():
         launches.append((kq, algo(["o"], HIDDEN), one("o", A["o"])))
         launches.append((kq, algo(["gate", "up"], HIDDEN), grp(["gate", "up"], A["ffn"])))
         launches.append((k6, algo(["down"], INTER), one("down", A["down"])))
+    return launches
 
-    def step(s):
+
+def run_set(qmv, hip, stream, launches, steps, warmup, use_graph):
+    """Warm up, then time `steps` steps (graph replays unless use_graph is
+    False) between two stream synchronisations; events between steps give
+    the per-step spread."""
+    sp = stream.handle
+
+    def step():
         for _, _, fn in launches:
-            if fn(s) != 1:
+            if fn(sp) != 1:
                 raise RuntimeError(qmv.last_error())
 
-    for _ in range(max(1, args.warmup)):
-        step(sp)
+    for _ in range(max(1, warmup)):
+        step()
     stream.synchronize()
-
     graph = None
-    if not args.no_graph:
+    if use_graph:
         graph = hip.Graph(stream)
         graph.begin()
-        step(sp)
+        step()
         graph.end()
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             graph.replay()
         stream.synchronize()
+    marks = [hip.Event() for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        marks[i].record(stream)
+        graph.replay() if graph is not None else step()
+    marks[steps].record(stream)
+    stream.synchronize()
+    elapsed = time.perf_counter() - t0
+    per_step = sorted(marks[i].elapsed_ms(marks[i + 1]) for i in range(steps))
+    eager = None
+    if graph is not None:
+        reps = max(3, steps // 5)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            step()
+        stream.synchronize()
+        eager = (time.perf_counter() - t0) / reps
+    q = lambda f: per_step[min(len(per_step) - 1, int(f * len(per_step)))]
+    return {"elapsed": elapsed, "ms_per_step": elapsed / steps * 1e3, "p10": q(0.1), "p50": q(0.5),
+            "p90": q(0.9), "eager_ms": eager * 1e3 if eager else None, "graph": graph is not None}
 
-    t_a = time.perf_counter()
-    for _ in range(args.steps):
-        if graph is not None:
+
+def launch_profile(hip, stream, launches, passes, use_graph):
+    """Average duration per launch of each kernel: the kernel's own launches
+    of one step, in step order, captured in a HIP graph and replayed `passes`
+    times between two HIP events on the launch stream (no event between
+    launches, so dispatch overhead is counted as in the timed replays).
+    Returns {kernel: [algorithmic bytes, ms, launches]} over all passes."""
+    per_kernel = {}
+    sp = stream.handle
+    for name in sorted({n for n, _, _ in launches}):
+        mine = [(b, fn) for n, b, fn in launches if n == name]
+        run = lambda: [fn(sp) for _, fn in mine]
+        graph = None
+        if use_graph:
+            graph = hip.Graph(stream)
+            graph.begin()
+            run()
+            graph.end()
             graph.replay()
         else:
-            step(sp)
-    stream.synchronize()
-    elapsed = time.perf_counter() - t_a
-
-    eager_elapsed = None
-    if graph is not None:
-        reps = max(3, args.steps // 5)
-        t_a = time.perf_counter()
-        for _ in range(reps):
-            step(sp)
+            run()
         stream.synchronize()
-        eager_elapsed = (time.perf_counter() - t_a) / reps
-
-    # ---- profiling pass: HIP events around every launch, on the bench stream
-    per_kernel = {}
-    kernel_sum = []
-    evs = [(hip.Event(), hip.Event()) for _ in launches]
-    for _ in range(args.profile_passes):
-        for (name, nbytes, fn), (e0, e1) in zip(launches, evs):
-            e0.record(stream)
-            fn(sp)
-            e1.record(stream)
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(stream)
+        for _ in range(passes):
+            graph.replay() if graph is not None else run()
+        e1.record(stream)
         stream.synchronize()
-        tot = 0.0
-        for (name, nbytes, _), (e0, e1) in zip(launches, evs):
-            ms = e0.elapsed_ms(e1)
-            tot += ms
-            d = per_kernel.setdefault(name, [0, 0.0, 0])
-            d[0] += nbytes
-            d[1] += ms
-            d[2] += 1
-        kernel_sum.append(tot)
+        per_kernel[name] = [passes * sum(b for b, _ in mine), e0.elapsed_ms(e1), passes * len(mine)]
+    return per_kernel
 
-    ms_per_step = elapsed / args.steps * 1e3
-    value = total_bytes / (elapsed / args.steps) / 1e9
-    dominant = max(per_kernel.items(), key=lambda kv: kv[1][1])
-    dname, (dbytes, dms, dcount) = dominant
+
+def committed_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by a copy-kernel
+    calibration), if it was taken on this kernel and workload."""
+    path = os.path.join(ROOT, "profiles", "roofline_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel or t.get("workload") != workload:
+        return None
+    return int(t["fetch_bytes_per_launch"] + t["write_bytes_per_launch"])
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1, help="positions per matvec (1 = decode, <= 8)")
+    ap.add_argument("--profile-passes", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the M=8 set and the read probe")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this path has no multi-GPU mode); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    if not 1 <= args.batch <= 8:
+        print("--batch must be in 1..8", file=sys.stderr)
+        sys.exit(2)
+
+    qmv = importlib.import_module("my-inference-engine_amd")
+    hip = importlib.import_module("my-inference-engine_amd.hip_runtime")
+    lib = qmv.hip_lib()
+    assert lib.qmv_device_count() > 0, "no GPU"
+    assert lib.qmv_set_device(0) == 1
+    hip.check(hip.rt().hipSetDevice(0), "hipSetDevice")
+    stream = hip.Stream()
+    M = args.batch
+    MX = max(M, 8)
+
+    # ---- weights: generated per layer on the host, uploaded, host copy dropped
+    t0 = time.time()
+    layers, host_layer0, total_bytes = [], None, 0
+    for layer in range(LAYERS):
+        tensors = {}
+        keep = []
+        for j, (name, t, rows, cols) in enumerate(layer_shapes()):
+            raw = qmv.synth_tensor(t, rows, cols, seed=1000 * layer + j)
+            total_bytes += raw.size
+            tensors[name] = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+            if layer == 0:
+                keep.append((name, t, rows, cols, raw))
+        if layer == 0:
+            host_layer0 = keep
+        layers.append(tensors)
+    upload_s = time.time() - t0
+
+    # ---- activations (fp32 N(0,1), token-major [MX, K] per layer) and
+    # outputs, resident in HBM; an M-position set reads the first M rows
+    acts, outs = [], []
+    for layer in range(LAYERS):
+        a = {k: hip.DeviceBuffer.from_array(qmv.synth_normal(MX * c, seed=50000 + 10 * layer + i))
+             for i, (k, c) in enumerate((("attn", HIDDEN), ("o", HIDDEN), ("ffn", HIDDEN), ("down", INTER)))}
+        o = {name: hip.DeviceBuffer(4 * MX * rows) for name, _, rows, _ in layer_shapes()}
+        acts.append(a)
+        outs.append(o)
+    hip.synchronize()
+
+    launches = build_launches(lib, layers, acts, outs, M)
+    main_run = run_set(qmv, hip, stream, launches, args.steps, args.warmup, not args.no_graph)
+    passes = max(1, args.profile_passes)
+    per_kernel = launch_profile(hip, stream, launches, passes, not args.no_graph)
+
+    value = total_bytes / (main_run["elapsed"] / args.steps) / 1e9
+    dname, (dbytes, dms, dcount) = max(per_kernel.items(), key=lambda kv: kv[1][1])
     achieved = (dbytes / dcount) / (dms / dcount * 1e-3) / 1e9
-    kernels = {k: {"launches_per_step": v[2] // args.profile_passes,
+    kernels = {k: {"launches_per_step": v[2] // passes,
                    "avg_bytes": v[0] // v[2], "avg_us": round(v[1] / v[2] * 1e3, 3),
                    "gbs": round((v[0] / v[2]) / (v[1] / v[2] * 1e-3) / 1e9, 1)} for k, v in per_kernel.items()}
+    workload = (f"Qwen2.5-7B-shaped decode-step projection set, M={M}: 28 layers x "
+                "{q,o 3584x3584; k,v 512x3584; gate,up 18944x3584 Q4_K; down 3584x18944 Q6_K}")
+
+    extra = {"per_step_ms_p10_p50_p90": [round(main_run[k], 4) for k in ("p10", "p50", "p90")],
+             "eager_ms_per_step": round(main_run["eager_ms"], 4) if main_run["eager_ms"] else None,
+             "kernel_sum_ms_per_step": round(sum(v[1] for v in per_kernel.values()) / passes, 4),
+             "kernels": kernels, "upload_s": round(upload_s, 2)}
+    if not args.no_extra:
+        if M != 8:
+            l8 = build_launches(lib, layers, acts, outs, 8)
+            r8 = run_set(qmv, hip, stream, l8, max(5, args.steps // 5), 2, not args.no_graph)
+            extra["m8_set"] = {"ms_per_step": round(r8["ms_per_step"], 4),
+                               "weight_gbs": round(total_bytes / (r8["elapsed"] / max(5, args.steps // 5)) / 1e9, 1),
+                               "positions_per_s": round(8 / (r8["ms_per_step"] * 1e-3), 1)}
+        probe = importlib.import_module("my-inference-engine_amd.probe")
+        extra["hbm_read_probe"] = probe.read_bandwidth(1 << 30, 512, 10)
+        extra["hbm_fraction_of_read_probe"] = round(value / extra["hbm_read_probe"]["gbs"], 4)
+
+    # ---- the drop-in host-pointer API (host x in, host y out, weights cached
+    # in HBM after the first call): PCIe-inclusive time per call, never `value`
+    host_api = {}
+    for name, t, rows, cols, raw in host_layer0 if not args.no_extra else []:
+        if name not in ("o", "gate", "down"):
+            continue
+        v = qmv.make_view(raw, t, rows, cols)
+        x = qmv.synth_normal(cols, seed=7000 + cols)
+        y = np.empty(rows, dtype=np.float32)
+        if qmv.quantized_tensor_matvec_f32(v, x, cols, y, rows) != 1:
+            raise RuntimeError(qmv.last_error())
+        reps = 50
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            qmv.quantized_tensor_matvec_f32(v, x, cols, y, rows)
+        host_api[name] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+        qmv.release_tensor(v.data)
+    if host_api:
+        extra["host_api_us_per_call"] = host_api
 
     cpu = None
     if not args.no_cpu:
@@ -231,27 +319,24 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(main_run["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: seeded Q4_K/Q6_K weights (d,dmin ~ |N(0,0.01)|, Q6_K d ~ |N(0,0.001)|), fp32 N(0,1) activations",
-        "config": {"workload": f"Qwen2.5-7B-shaped decode-step projection set, M={M}: 28 layers x "
-                               "{q,o 3584x3584; k,v 512x3584; gate,up 18944x3584 Q4_K; down 3584x18944 Q6_K}",
-                   "batch": M, "layers": LAYERS, "packed_weight_bytes": total_bytes,
-                   "launches_per_step": len(launches), "hip_graph": graph is not None},
-        "us_per_set": round(ms_per_step * 1e3, 1),
+        "config": {"workload": workload, "batch": M, "layers": LAYERS, "packed_weight_bytes": total_bytes,
+                   "launches_per_step": len(launches), "hip_graph": main_run["graph"]},
+        "us_per_set": round(main_run["ms_per_step"] * 1e3, 1),
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dname,
-                     "bytes_per_launch": dbytes // dcount, "avg_launch_us": round(dms / dcount * 1e3, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dname, workload),
+                     "kernel": dname, "bytes_per_launch": dbytes // dcount,
+                     "avg_launch_us": round(dms / dcount * 1e3, 3)},
         "cpu_baseline": cpu,
-        "extra": {"eager_ms_per_step": round(eager_elapsed * 1e3, 4) if eager_elapsed else None,
-                  "kernel_sum_ms_per_step": round(statistics.median(kernel_sum), 4),
-                  "kernels": kernels, "upload_s": round(upload_s, 2)},
+        "extra": extra,
     }
-    print(json.dumps(out))
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -400,3 +400,34 @@ def test_reference_avx2_build_within_tolerance(oracle, t):
     _, absdot = oracle.row_stats(raw, t, rows, cols, x)
     ok = np.isfinite(absdot)
     assert np.all(np.abs(ours[ok] - theirs[ok]) <= 1e-5 * absdot[ok])
+
+
+# ---- row-range helpers used as the GPU checker ---------------------------------
+
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+def test_row_helpers_against_independent_forms(oracle, t):
+    """oracle_dequantize_rows is the per-block decoder (pinned above) laid out
+    row by row; oracle_matvec_rows_f32 is a slice of the full matvec bit for
+    bit; oracle_row_stats_f64 equals a float64 numpy dot over the decoded rows
+    (sum of w*x and of |w*x|), so the tolerance denominator is pinned too."""
+    be, bpr, rows = B.BLOCK_ELEMENTS[t], 6, 23
+    cols = bpr * be
+    raw = B.raw_blocks(t, rows * bpr, seed=900 + t)
+    bb = B.BLOCK_BYTES[t]
+    blocks = [raw[i * bb:(i + 1) * bb] for i in range(rows * bpr)]
+    w = np.stack([np.concatenate([_dq(oracle, t, blocks[r * bpr + b]) for b in range(bpr)]) for r in range(rows)])
+    got = oracle.dequantize_rows(raw, t, rows, cols, 5, 11)
+    nan = np.isnan(w[5:16])
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), w[5:16][~nan].view(np.uint32))
+
+    x = np.random.default_rng(t).standard_normal(cols).astype(np.float32)
+    full = oracle.matvec(raw, t, rows, cols, x)
+    part = oracle.matvec_rows(raw, t, rows, cols, x, 7, 9)
+    assert np.array_equal(part.view(np.uint32), full[7:16].view(np.uint32))
+
+    dot, absdot = oracle.row_stats(raw, t, rows, cols, x, 3, 17)
+    prod = w[3:20].astype(np.float64) * x.astype(np.float64)
+    fin = np.isfinite(prod).all(axis=1)
+    assert np.allclose(dot[fin], prod[fin].sum(axis=1), rtol=1e-12, atol=1e-300)
+    assert np.allclose(absdot[fin], np.abs(prod[fin]).sum(axis=1), rtol=1e-12, atol=1e-300)
