@@ -1,6 +1,6 @@
 """ORACLE — test infrastructure only.
 
-ctypes access to the CPU checker for the MI355X packed matvec path:
+ctypes access to the CPU oracle for the MI355X packed matvec path:
   * ``liboracle.so``: the plain-C restatement of the reference's scalar path
     (qmv_oracle.c; header qmv_oracle.h lists what pins each function);
   * ``_ref/libref_scalar.so`` / ``_ref/libref_avx2.so``: the reference's own

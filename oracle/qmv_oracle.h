@@ -3,7 +3,7 @@
  *
  * A plain-C restatement of the reference engine's CPU packed-weight path
  * (trungnguyen21/my-inference-engine, src/quantization.cpp scalar branches and
- * src/quantized_matvec.cpp), used as the checker for the MI355X kernels.
+ * src/quantized_matvec.cpp), against which the MI355X kernels are tested.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it, and only to check or to time a CPU baseline; the product library
  * (libqmv_hip.so) never links or calls it.

@@ -90,7 +90,7 @@ def test_invalid_arguments_fail_without_gpu(qmv):
     assert y[0] == 0.0
 
 
-def test_config2_q4_k_shape_rejected_without_gpu(qmv):
+def test_q4_k_4864x896_rejected_without_gpu(qmv):
     """Q4_K 4864 x 896 (K not a multiple of 256) must return 0 like the reference."""
     raw = np.zeros(16, dtype=np.uint8)
     v = qmv.make_view(raw, B.Q4_K, 4864, 896)

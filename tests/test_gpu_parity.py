@@ -199,7 +199,7 @@ def test_invalid_arguments_leave_output(qmv, gpu):
     assert qmv.quantized_tensor_matmul_f32(v, x, 32, 0, y, 1) == 0
     assert (y == -7.0).all()
     raw = np.zeros(16, dtype=np.uint8)
-    v = qmv.make_view(raw, B.Q4_K, 4864, 896)  # config 2's Q4_K shape: K % 256 != 0
+    v = qmv.make_view(raw, B.Q4_K, 4864, 896)  # Q4_K 4864x896: K % 256 != 0
     assert qmv.quantized_tensor_matvec_f32(v, np.zeros(896, np.float32), 896, np.zeros(4864, np.float32), 4864) == 0
 
 
@@ -222,26 +222,26 @@ def test_failure_injection_publishes_nothing(qmv, gpu):
 
 # ---- parity at the workload shapes ----------------------------------------------------------
 
-def test_config1_q8_0_896(qmv, oracle, gpu):
+def test_q8_0_896x896_q_proj(qmv, oracle, gpu):
     x = qmv.synth_normal(896, seed=0).reshape(1, 896)
-    matvec_parity(qmv, oracle, B.Q8_0, 896, 896, seed=0, x=x, what="C1 Q8_0")
+    matvec_parity(qmv, oracle, B.Q8_0, 896, 896, seed=0, x=x, what="Q8_0 896x896")
 
 
-def test_config2_q6_k_down(qmv, oracle, gpu):
-    matvec_parity(qmv, oracle, B.Q6_K, 896, 4864, seed=2, what="C2 Q6_K down")
+def test_q6_k_896x4864_down(qmv, oracle, gpu):
+    matvec_parity(qmv, oracle, B.Q6_K, 896, 4864, seed=2, what="Q6_K 896x4864")
 
 
 @pytest.mark.parametrize("t,rows,cols", [(B.Q5_0, 1536, 1536), (B.Q5_0, 256, 1536), (B.Q4_K, 8960, 1536),
                                          (B.Q4_K, 1536, 8960)])
-def test_config3_prefill_m8(qmv, oracle, gpu, t, rows, cols):
-    matvec_parity(qmv, oracle, t, rows, cols, batch=8, seed=3, what="C3 M=8")
+def test_qwen2_1_5b_prefill_m8(qmv, oracle, gpu, t, rows, cols):
+    matvec_parity(qmv, oracle, t, rows, cols, batch=8, seed=3, what="1.5B prefill M=8")
 
 
 @pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 3584, 3584), (B.Q4_K, 512, 3584), (B.Q4_K, 18944, 3584),
                                          (B.Q6_K, 3584, 18944)])
 @pytest.mark.parametrize("batch", [1, 8])
-def test_config5_layer_shapes(qmv, oracle, gpu, t, rows, cols, batch):
-    matvec_parity(qmv, oracle, t, rows, cols, batch=batch, seed=5, what="C5")
+def test_qwen2_7b_layer_shapes(qmv, oracle, gpu, t, rows, cols, batch):
+    matvec_parity(qmv, oracle, t, rows, cols, batch=batch, seed=5, what="7B layer")
 
 
 @pytest.mark.parametrize("t", B.ALL_TYPES)
@@ -278,7 +278,7 @@ def test_launch_plans_match_oracle(qmv, oracle, gpu, plan, t):
         qmv.set_launch_tuning(0, 0, 0)
 
 
-def test_config4_vocab_projection_and_argmax(qmv, oracle, gpu):
+def test_vocab_151936x3584_projection_and_argmax(qmv, oracle, gpu):
     """Q6_K 151936 x 3584 (446 MB) then greedy argmax: the index equals the
     CPU argmax of the oracle's logits."""
     rows, cols = 151936, 3584
@@ -295,7 +295,7 @@ def test_config4_vocab_projection_and_argmax(qmv, oracle, gpu):
     srt = np.sort(y_ref)
     gap = float(srt[-1] - srt[-2])
     bound = 2 * TOL * float(absdot[tok_cpu])
-    log(f"C4 argmax {tok_cpu}: top-2 gap {gap:.3e} vs row error bound {bound:.3e}")
+    log(f"vocab argmax {tok_cpu}: top-2 gap {gap:.3e} vs row error bound {bound:.3e}")
     assert tok_gpu == tok_cpu
     assert qmv.greedy_sample(y_ref) == (1, tok_cpu)
     qmv.release_tensor(v.data)

@@ -310,7 +310,7 @@ def test_invalid_arguments(oracle):
     assert lib.oracle_matvec_f32(vp, _p(x), 32, _p(y), 1) == 1
 
 
-def test_config2_q4_k_shape_is_rejected(oracle):
+def test_q4_k_4864x896_is_rejected(oracle):
     """Q4_K 4864 x 896: 896 is not a multiple of 256 (src/quantized_matvec.cpp:136-138)."""
     raw = np.zeros(1, dtype=np.uint8)
     v = oracle.view(raw, B.Q4_K, 4864, 896)
@@ -402,7 +402,7 @@ def test_reference_avx2_build_within_tolerance(oracle, t):
     assert np.all(np.abs(ours[ok] - theirs[ok]) <= 1e-5 * absdot[ok])
 
 
-# ---- row-range helpers used as the GPU checker ---------------------------------
+# ---- row-range helpers used by the GPU parity tests -----------------------------
 
 @pytest.mark.parametrize("t", B.ALL_TYPES)
 def test_row_helpers_against_independent_forms(oracle, t):
