@@ -166,17 +166,19 @@ int qmv_device_count(void);
  * argument). A launch gives each workgroup one 64-row tile and a contiguous
  * range of K-units, processed by waves_per_group waves of units_per_wave
  * units each (default: 1 unit, 4 waves, or 8 for rows of 32 or more
- * K-units); a tile's K is split across
- * workgroups as far as that requires, and the last split to finish adds the
- * partials in split order. target_waves, if set, instead grows the units per
- * wave until about that many waves cover the launch. Defaults may also come
- * from the QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP
- * environment variables. Any setting stays within the row tolerance: the plan
- * only changes the summation order, and a given plan always sums in the same
- * order.
+ * K-units); a tile's K is split across workgroups as far as that requires,
+ * and the last split to finish adds the partials in split order.
+ * target_waves, if set, instead grows the units per wave until about that
+ * many waves cover the launch. Q4_K and Q6_K batches of at least
+ * mfma_min_batch positions (default 7 for Q4_K, 8 for Q6_K; a value above
+ * QMV_MAX_BATCH turns it off) run on the matrix cores. Defaults may also come from the
+ * QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP /
+ * QMV_MFMA_MIN_BATCH environment variables. Any setting stays within the row
+ * tolerance: the plan only changes the summation order, and a given plan
+ * always sums in the same order.
  */
 void qmv_set_launch_tuning(int target_waves, int units_per_wave,
-                           int waves_per_group);
+                           int waves_per_group, int mfma_min_batch);
 
 /*
  * Test hook for failure propagation (the role of the reference's link-time

@@ -102,7 +102,7 @@ HIP_SIGNATURES = {
     "qmv_set_device": (ctypes.c_int, [ctypes.c_int]),
     "qmv_device_count": (ctypes.c_int, []),
     "qmv_debug_fail_next_calls": (None, [ctypes.c_int]),
-    "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
 }
 
 SYNTH_SIGNATURES = {
@@ -203,9 +203,10 @@ def greedy_sample(logits: np.ndarray):
     return ok, tok.value
 
 
-def set_launch_tuning(target_waves: int = 0, units_per_wave: int = 0, waves_per_group: int = 0) -> None:
+def set_launch_tuning(target_waves: int = 0, units_per_wave: int = 0, waves_per_group: int = 0,
+                      mfma_min_batch: int = 0) -> None:
     """Process-wide launch-plan override (0 = automatic); see qmv_hip.h."""
-    hip_lib().qmv_set_launch_tuning(target_waves, units_per_wave, waves_per_group)
+    hip_lib().qmv_set_launch_tuning(target_waves, units_per_wave, waves_per_group, mfma_min_batch)
 
 
 def register_tensor(view: QmvTensorView) -> int:

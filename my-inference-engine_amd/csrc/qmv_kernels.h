@@ -38,6 +38,7 @@ struct MatvecParams {
     int units_per_wave; /* contiguous K-units per wave */
     float *partials;
     unsigned *counters; /* all zero between launches */
+    int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
 };
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);

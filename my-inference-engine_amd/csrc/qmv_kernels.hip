@@ -711,6 +711,79 @@ template <int FMT, int M> struct MatvecOccupancy {
     static constexpr int value = M == 1 ? QMV_WAVES_PER_SIMD_M1 : QMV_WAVES_PER_SIMD_MN;
 };
 
+/* The workgroup's place in a launch: job, tile, K-split, and this wave's
+ * K-units [u_begin, u_end). */
+struct WgWork {
+    int job, tile, split, u_begin, u_end;
+};
+
+__device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave)
+{
+    WgWork w;
+    int j = 0;
+    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const MatvecJob &job = p.job[j];
+    const int local = blockIdx.x - job.wg_begin;
+    w.job = j;
+    w.tile = local / job.splits;
+    w.split = local - w.tile * job.splits;
+    const int split_begin = w.split * job.units_per_split;
+    const int split_end = min(split_begin + job.units_per_split, p.units);
+    w.u_begin = split_begin + wave * p.units_per_wave;
+    w.u_end = min(w.u_begin + p.units_per_wave, split_end);
+    return w;
+}
+
+/* After every wave has written red[wave][m][row] (row = tile row 0..63) and
+ * the workgroup has synchronised, wave 0 adds the waves in wave order and
+ * stores the rows, or, for a tile split along K, publishes this split's
+ * partial; the last split to arrive adds all partials of the tile in split
+ * order (a fixed order, so results do not depend on arrival order).
+ * Partials and counters are accessed only with agent-scope atomics, which are
+ * coherent across the XCDs' L2s without a cache writeback or invalidate: the
+ * wait for the partial stores to complete orders them before the arrival
+ * count. The last split resets the counter, so the workspace needs no
+ * clearing between launches. */
+template <int M>
+__device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork &w, int nwaves, int lane,
+                                            const float (*red)[M][64])
+{
+    const MatvecJob &job = p.job[w.job];
+    float sum[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float s = red[0][m][lane];
+        for (int v = 1; v < nwaves; ++v) s += red[v][m][lane];
+        sum[m] = s;
+    }
+    const int row = w.tile * 64 + lane;
+
+    if (job.splits == 1) {
+        if (row < job.rows) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = sum[m];
+        }
+        return;
+    }
+
+    float *part = p.partials + job.partial_offset + ((size_t)w.tile * job.splits) * M * 64;
+    unsigned *count = p.counters + job.counter_offset + w.tile;
+#pragma unroll
+    for (int m = 0; m < M; ++m) store_partial(part + ((size_t)w.split * M + m) * 64 + lane, sum[m]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+    if (prev != (unsigned)job.splits - 1u) return;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float s = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
+        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
+    }
+    if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 /* kOne: every wave takes at most one unit (units_per_wave == 1), so no
  * second unit buffer is live and more waves fit per SIMD. */
 template <int FMT, int M, bool kOne>
@@ -724,90 +797,293 @@ matvec_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nwaves = blockDim.x >> 6;
-
-    int j = 0;
-    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
-    const MatvecJob &job = p.job[j];
-    const int local = blockIdx.x - job.wg_begin;
-    const int tile = local / job.splits;
-    const int split = local - tile * job.splits;
-
-    const int split_begin = split * job.units_per_split;
-    const int split_end = min(split_begin + job.units_per_split, p.units);
-    const int u_begin = split_begin + wave * p.units_per_wave;
-    const int u_end = min(u_begin + p.units_per_wave, split_end);
-
-    const uint8_t *wtile = job.w + (size_t)tile * p.units * SLAB;
+    const WgWork w = locate(p, wave);
+    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
     if (kOne) {
-        if (u_begin < u_end) {
+        if (w.u_begin < w.u_end) {
             Unit a;
-            load_unit(a, wtile + (size_t)u_begin * SLAB, lane);
-            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u_begin, lane, acc);
+            load_unit(a, wtile + (size_t)w.u_begin * SLAB, lane);
+            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, w.u_begin, lane, acc);
         }
-    } else if (u_begin < u_end) {
+    } else if (w.u_begin < w.u_end) {
         /* Two units in flight per wave: the next unit's planes are loading
          * while the current one is decoded. */
         Unit a, b;
-        load_unit(a, wtile + (size_t)u_begin * SLAB, lane);
-        for (int u = u_begin; u < u_end; u += 2) {
-            const bool has_b = u + 1 < u_end;
+        load_unit(a, wtile + (size_t)w.u_begin * SLAB, lane);
+        for (int u = w.u_begin; u < w.u_end; u += 2) {
+            const bool has_b = u + 1 < w.u_end;
             if (has_b) load_unit(b, wtile + (size_t)(u + 1) * SLAB, lane);
             unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u, lane, acc);
-            if (u + 2 < u_end) load_unit(a, wtile + (size_t)(u + 2) * SLAB, lane);
+            if (u + 2 < w.u_end) load_unit(a, wtile + (size_t)(u + 2) * SLAB, lane);
             if (has_b) unit_step<FMT, M>(b, p.x, p.ldx, p.cols, u + 1, lane, acc);
         }
     }
 
-    /* Combine the waves of this workgroup in wave order. */
 #pragma unroll
     for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
     __syncthreads();
     if (wave != 0) return;
+    finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
+}
 
-    float sum[M];
+/* ---- M >= 2 on the matrix cores (Q4_K, Q6_K) ---------------------------------
+ * Over one scale sub-block a row contributes a * sum(q * x) (- b * sum(x) for
+ * Q4_K's minimum), with q the integer codes, exact in bf16. Each activation
+ * is split into three bf16 limbs, x = h + m + l with h = bf16(x),
+ * m = bf16(x - h), l = bf16(x - h - m): each difference is exact in fp32 and
+ * l takes the remaining bits, so the limbs carry x exactly. bf16 MFMA
+ * products are exact and accumulate in fp32, so sum(q * x) is an fp32 sum of
+ * exact products, as on the VALU path, with the codes decoded once for up to
+ * 8 positions.
+ *
+ * MFMA operand roles (lane l, kc = l / 16, n = l % 16): A = limbs, row i =
+ * position (rows >= M are zero), lane l supplies A[n][kc*KL + j]; B = weight
+ * codes, column = weight row 16g + n of row group g, lane l supplies
+ * B[kc*KL + j][n]; D[i][n] lands in lane n + 16*(i/4), element i % 4. So a
+ * lane's accumulator holds positions 4*kc..4*kc+3 of one weight row, and the
+ * per-row scales it applies are that row's own. KL = 8 (16x16x32 MFMA, Q4_K
+ * sub-blocks of 32) or 4 (16x16x16, Q6_K sub-blocks of 16). Per sub-block the
+ * MFMAs of the four row groups are issued limb by limb, so four (five with
+ * Q4_K's sum(x)) independent accumulations keep the matrix pipe busy. */
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
+
+/* A per-lane pointer that cannot be used before `dep` exists: ties the
+ * activation loads of a sub-block to the accumulators of an earlier one, so
+ * the loads are not all hoisted to the top of the unrolled unit. */
+__device__ __forceinline__ const float *ptr_after(const float *p, float dep)
+{
+    asm("" : "+v"(p) : "v"(dep));
+    return p;
+}
+
+template <int KL>
+__device__ __forceinline__ void load_x(float (&v)[KL], const float *p)
+{
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float s = red[0][m][lane];
-        for (int w = 1; w < nwaves; ++w) s += red[w][m][lane];
-        sum[m] = s;
+    for (int j = 0; j < KL; ++j) v[j] = p[j];
+}
+
+/* The three bf16 limbs of KL activations of one position (zero when the lane
+ * carries no position). */
+template <int KL, typename V>
+__device__ __forceinline__ void x_limbs(const float (&xv)[KL], bool valid, V &h, V &m, V &l)
+{
+#pragma unroll
+    for (int j = 0; j < KL; ++j) {
+        const float v = valid ? xv[j] : 0.0f;
+        const __bf16 vh = (__bf16)v;
+        const float r = v - (float)vh;
+        const __bf16 vm = (__bf16)r;
+        h[j] = vh;
+        m[j] = vm;
+        l[j] = (__bf16)(r - (float)vm);
     }
-    const int row = tile * 64 + lane;
+}
 
-    if (job.splits == 1) {
-        if (row < job.rows) {
+template <int M>
+__device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
+                                              f32x4_t (&acc)[4])
+{
+    const int kc = lane >> 4, n = lane & 15;
+    const bool valid = n < M;
+    /* Lanes past the batch read position 0 (in bounds) and use zeros. */
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
+    /* This lane's bytes of row 16g + n: header, and the 8 qs bytes of its
+     * k-chunk in 64-weight group c (plane 1 + 2c + kc/2). */
+    const uint8_t *rowp = slab + n * 16;
+    const uint8_t *qsp = slab + (1 + (kc >> 1)) * 1024 + n * 16 + 8 * (kc & 1);
+    uint4 h[4];
 #pragma unroll
-            for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = sum[m];
+    for (int g = 0; g < 4; ++g) h[g] = ld16(rowp + g * 256);
+    uint2 q[2][4]; /* codes of group c and c + 1 */
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[0][g] = *(const uint2 *)(qsp + g * 256);
+    const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
+                           (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+    float xv[2][8];
+    load_x<8>(xv[0], xp);
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+        const int c = sb >> 1;
+        const bool high = sb & 1;
+        /* Next sub-block's activations, and at a group's start the next
+         * group's codes, load while this sub-block runs. */
+        if (sb + 1 < 8) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
+        if (!high && c + 1 < 4) {
+            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
         }
-        return;
+        bf16x8_t a0, a1, a2;
+        x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
+        /* High nibbles are used in place as 16 * q; 1/16 is folded into the
+         * sub-block scale (exact). */
+        const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        bf16x8_t b[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lo = codes(after(q[c & 1][g].x, acc[g][0]) & mask);
+            const uint32_t hi = codes(after(q[c & 1][g].y, acc[g][0]) & mask);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                b[g][j] = (__bf16)ubyte(lo, j);
+                b[g][4 + j] = (__bf16)ubyte(hi, j);
+            }
+        }
+        f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            /* Decoded here, not hoisted: the scales of one sub-block live. */
+            const float dep = d[g][0];
+            const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep), after(h[g].w, dep)};
+            const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
+            uint32_t scw, mw;
+            if (sb < 4) {
+                scw = hg.y & 0x3f3f3f3fu;
+                mw = hg.z & 0x3f3f3f3fu;
+            } else {
+                scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
+                mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
+            }
+            float sa = dd * ubyte(scw, sb & 3);
+            if (high) sa *= 0.0625f;
+            const float sm = dmin * ubyte(mw, sb & 3);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] = fmaf(sa, d[g][j], fmaf(-sm, xs[j], acc[g][j]));
+        }
+    }
+}
+
+/* Q6_K sub-block j = 8G + 2r + hf (16 weights) takes its low nibbles from
+ * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
+ * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
+ * ql/qh words serves four of them. */
+template <int M>
+__device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
+                                              f32x4_t (&acc)[4])
+{
+    const int kc = lane >> 4, n = lane & 15;
+    const bool valid = n < M;
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 4 * kc;
+    const uint8_t *wp = slab + n * 16 + 4 * kc; /* this lane's dword of row 16g + n in a plane */
+    uint4 sc[4];
+    float dg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        sc[g] = ld16(slab + 12 * 1024 + (16 * g + n) * 16);
+        dg[g] = f16_bits_to_f32(*(const unsigned short *)(slab + 13312 + (16 * g + n) * 2));
+    }
+    /* Words of pair (G, hf) and the next pair: ql for r & 1 = 0, 1 and qh. */
+    uint32_t w[2][4][3];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        w[0][g][0] = *(const uint32_t *)(wp + 0 * 1024 + g * 256);
+        w[0][g][1] = *(const uint32_t *)(wp + 2 * 1024 + g * 256);
+        w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
+    }
+    float xv[2][4];
+    load_x<4>(xv[0], xp);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
+        const int G = pr >> 1, hf = pr & 1;
+        const int j = 8 * G + 2 * r + hf;
+        if (t + 1 < 16) {
+            const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
+            load_x<4>(xv[(t + 1) & 1], ptr_after(xp + 16 * jn, acc[0][0]));
+        }
+        if (r == 0 && pr + 1 < 4) {
+            const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
+            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                w[(pr + 1) & 1][g][0] = *(const uint32_t *)(np + (4 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][1] = *(const uint32_t *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
+            }
+        }
+        bf16x4_t a0, a1, a2;
+        x_limbs<4>(xv[t & 1], valid, a0, a1, a2);
+        bf16x4_t b[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[g][0]);
+            const uint32_t hw = after(w[pr & 1][g][2], acc[g][0]);
+            const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
+        }
+        f32x4_t d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float s = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(s, d[g][i], acc[g][i]);
+        }
+    }
+}
+
+/* Same launch plan, combine and split-K protocol as matvec_kernel; each wave
+ * runs its units on the matrix cores and scatters its 64 rows x M positions
+ * into the combine buffer. */
+/* Four resident waves per SIMD (at most 128 VGPRs): these waves are short
+ * and latency-bound, so residency matters more than registers. */
+template <int FMT, int M>
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
+matvec_mfma_kernel(MatvecParams p)
+{
+    constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    __shared__ float red[QMV_MAX_WAVES][M][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgWork w = locate(p, wave);
+    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
+
+    f32x4_t acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = w.u_begin; u < w.u_end; ++u) {
+        if constexpr (FMT == QMV_FMT_Q4_K)
+            q4k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+        else
+            q6k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
     }
 
-    /* Split K: publish this split's partial, the last split to arrive adds
-     * all partials of the tile in split order (a fixed order, so results do
-     * not depend on arrival order). Partials and counters are accessed only
-     * with agent-scope atomics, which are coherent across the XCDs' L2s
-     * without a cache writeback or invalidate: the wait for the partial
-     * stores to complete orders them before the arrival count. */
-    float *part = p.partials + job.partial_offset + ((size_t)tile * job.splits) * M * 64;
-    unsigned *count = p.counters + job.counter_offset + tile;
+    const int kc = lane >> 4, n = lane & 15;
 #pragma unroll
-    for (int m = 0; m < M; ++m) store_partial(part + ((size_t)split * M + m) * 64 + lane, sum[m]);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
-    if (prev != (unsigned)job.splits - 1u) return;
-    asm volatile("" ::: "memory");
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float s = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
-        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
-    }
-    if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < 4; ++j)
+            if (4 * kc + j < M) red[wave][4 * kc + j][16 * g + n] = acc[g][j];
+    __syncthreads();
+    if (wave != 0) return;
+    finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------
@@ -952,6 +1228,12 @@ argmax_stage2(const float *__restrict__ bval, const int *__restrict__ bidx, cons
 template <int FMT, int M>
 static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
 {
+    if constexpr (M >= 2 && (FMT == QMV_FMT_Q4_K || FMT == QMV_FMT_Q6_K)) {
+        if (p.matrix_cores) {
+            hipLaunchKernelGGL((matvec_mfma_kernel<FMT, M>), dim3(grid), dim3(waves * 64), 0, s, p);
+            return hipGetLastError();
+        }
+    }
     if (p.units_per_wave == 1)
         hipLaunchKernelGGL((matvec_kernel<FMT, M, true>), dim3(grid), dim3(waves * 64), 0, s, p);
     else

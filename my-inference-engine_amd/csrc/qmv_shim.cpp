@@ -152,7 +152,9 @@ struct Workspace {
     std::mutex mu;
 };
 
-/* Grow the workspace; waits for work already queued on the stream. */
+/* Grow the workspace; waits for work already queued on the stream. New
+ * counters are zeroed on the stream the kernels run on (never inside a graph
+ * capture: growth is refused there), so every launch finds them zero. */
 int workspace_reserve(Workspace &ws, hipStream_t stream, size_t partials, size_t counters)
 {
     if (partials <= ws.partial_cap && counters <= ws.counter_cap) return 1;
@@ -176,7 +178,7 @@ int workspace_reserve(Workspace &ws, hipStream_t stream, size_t partials, size_t
         ws.counters = nullptr;
         ws.counter_cap = 0;
         HIP_TRY(hipMalloc(&ws.counters, n * sizeof(unsigned)));
-        HIP_TRY(hipMemset(ws.counters, 0, n * sizeof(unsigned)));
+        HIP_TRY(hipMemsetAsync(ws.counters, 0, n * sizeof(unsigned), stream));
         ws.counter_cap = n;
     }
     return 1;
@@ -380,6 +382,18 @@ int env_int(const char *name, int dflt)
 std::atomic<int> g_target_waves{env_int("QMV_TARGET_WAVES", 0)};
 std::atomic<int> g_force_u{env_int("QMV_UNITS_PER_WAVE", 0)};
 std::atomic<int> g_force_w{env_int("QMV_WAVES_PER_GROUP", 0)};
+/* Smallest batch run on the matrix cores (Q4_K, Q6_K); above QMV_MAX_BATCH
+ * turns them off. By default the batch from which they beat the VALU path on
+ * MI355X at Qwen2.5-7B layer shapes: 7 for Q4_K, 8 for Q6_K (its code
+ * assembly costs more VALU per weight on the matrix-core path). */
+std::atomic<int> g_mfma_min_batch{env_int("QMV_MFMA_MIN_BATCH", 0)};
+
+bool use_matrix_cores(int fmt, int batch)
+{
+    if (fmt != QMV_FMT_Q4_K && fmt != QMV_FMT_Q6_K) return false;
+    const int t = g_mfma_min_batch.load();
+    return batch >= (t > 0 ? t : fmt == QMV_FMT_Q4_K ? 7 : 8);
+}
 
 struct Plan {
     int units_per_wave, waves, splits, units_per_split;
@@ -462,6 +476,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         set_error("launch too large");
         return 0;
     }
+    p.matrix_cores = use_matrix_cores(t0->geo.format, batch);
     std::lock_guard<std::mutex> lock(ws.mu);
     if (!workspace_reserve(ws, stream, partials, counters)) return 0;
     p.partials = ws.partials;
@@ -733,8 +748,10 @@ QMV_API int qmv_device_count(void)
     return n;
 }
 
-QMV_API void qmv_set_launch_tuning(int target_waves, int units_per_wave, int waves_per_group)
+QMV_API void qmv_set_launch_tuning(int target_waves, int units_per_wave, int waves_per_group,
+                                   int mfma_min_batch)
 {
+    g_mfma_min_batch.store(mfma_min_batch > 0 ? mfma_min_batch : 0);
     g_target_waves.store(target_waves > 0 ? target_waves : 0);
     g_force_u.store(units_per_wave > 0 ? units_per_wave : 0);
     g_force_w.store(waves_per_group > 0 && waves_per_group <= QMV_MAX_WAVES ? waves_per_group : 0);

@@ -257,11 +257,14 @@ def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
     matvec_parity(qmv, oracle, t, rows, cols, seed=rows + cols, what="odd shape")
 
 
-# Launch plans: (target_waves, units_per_wave, waves_per_group). The default
-# gives every wave one unit (the single-unit kernel variant); the others run
-# the two-unit pipelined variant, one wave per workgroup, whole-K workgroups
-# (no split) and target-sized units.
-PLANS = [(0, 0, 0), (0, 2, 0), (0, 3, 7), (0, 1, 1), (0, 1, 8), (2048, 0, 0), (0, 2, 1), (0, 8, 8), (0, 5, 3)]
+# Launch plans: (target_waves, units_per_wave, waves_per_group,
+# mfma_min_batch). The default gives every wave one unit (the single-unit
+# kernel variant) and runs Q4_K batches of 7 or more and Q6_K batches of 8 on
+# the matrix cores; the others run the two-unit pipelined variant, one wave per
+# workgroup, whole-K workgroups (no split), target-sized units, the VALU path
+# for every batch (mfma_min_batch 9) and the matrix cores from batch 2.
+PLANS = [(0, 0, 0, 0), (0, 2, 0, 0), (0, 3, 7, 0), (0, 1, 1, 0), (0, 1, 8, 0), (2048, 0, 0, 0), (0, 2, 1, 0),
+         (0, 8, 8, 0), (0, 5, 3, 0), (0, 0, 0, 9), (0, 2, 0, 9), (0, 3, 7, 9), (0, 0, 0, 2), (0, 2, 0, 2)]
 
 
 @pytest.mark.parametrize("plan", PLANS)
@@ -275,7 +278,7 @@ def test_launch_plans_match_oracle(qmv, oracle, gpu, plan, t):
         for batch in (1, 3, 8):
             matvec_parity(qmv, oracle, t, 130, cols, batch=batch, seed=batch + 40, what=f"plan {plan}")
     finally:
-        qmv.set_launch_tuning(0, 0, 0)
+        qmv.set_launch_tuning(0, 0, 0, 0)
 
 
 def test_vocab_151936x3584_projection_and_argmax(qmv, oracle, gpu):
