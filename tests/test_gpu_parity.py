@@ -419,29 +419,31 @@ def test_group_launch_matches_oracle(qmv, oracle, gpu, hip):
         d.close()
 
 
-def test_graph_replays_match_eager(qmv, gpu, hip):
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 3584, 18944, 1), (B.Q4_K, 3584, 3584, 8),
+                                               (B.Q6_K, 896, 4864, 8), (B.Q4_K, 512, 3584, 3)])
+def test_graph_replays_match_eager(qmv, gpu, hip, t, rows, cols, batch):
     """A captured launch (split-K counters reset by the kernel itself, no
-    memset nodes) replays to the eager result, with host work in between."""
-    t, rows, cols = B.Q6_K, 3584, 18944
+    memset nodes) replays to the eager result, with host work in between; at
+    M = 8 the launch runs on the matrix cores."""
     raw = qmv.synth_tensor(t, rows, cols, seed=61)
     dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
-    x = qmv.synth_normal(cols, seed=62)
+    x = qmv.synth_normal(batch * cols, seed=62)
     dx = hip.DeviceBuffer.from_array(x)
-    dy = hip.DeviceBuffer(4 * rows)
+    dy = hip.DeviceBuffer(4 * rows * batch)
     stream = hip.Stream()
-    dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)  # sizes the stream's workspace
+    dt.matvec(dx.ptr, batch, dy.ptr, stream.handle)  # sizes the stream's workspace
     stream.synchronize()
-    eager = dy.to_array(np.float32, (rows,))
+    eager = dy.to_array(np.float32, (batch * rows,))
     g = hip.Graph(stream)
     g.begin()
-    dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)
+    dt.matvec(dx.ptr, batch, dy.ptr, stream.handle)
     g.end()
     for i in range(5):
         dy.fill(0)
         g.replay()
         stream.synchronize()
-        assert np.array_equal(dy.to_array(np.float32, (rows,)).view(np.uint32), eager.view(np.uint32)), i
-        dt.matvec(dx.ptr, 1, dy.ptr, stream.handle)  # eager work between replays
+        assert np.array_equal(dy.to_array(np.float32, (batch * rows,)).view(np.uint32), eager.view(np.uint32)), i
+        dt.matvec(dx.ptr, batch, dy.ptr, stream.handle)  # eager work between replays
         stream.synchronize()
     dt.close()
 
