@@ -186,6 +186,48 @@ def launch_profile(hip, stream, launches, passes, use_graph):
     return per_kernel
 
 
+def vocab_bench(qmv, hip, stream, reps):
+    """Vocabulary projection 151936 x 3584 Q6_K at M=1 followed by greedy
+    sampling: the matvec alone, matvec + separate device argmax, and the
+    fused launch; each from graph replays between two HIP events."""
+    rows, cols = 151936, 3584
+    raw = qmv.synth_tensor(Q6_K, rows, cols, seed=77)
+    nbytes = raw.size
+    dt = qmv.DeviceTensor(qmv.make_view(raw, Q6_K, rows, cols))
+    del raw
+    dx = hip.DeviceBuffer.from_array(qmv.synth_normal(cols, seed=78))
+    dl = hip.DeviceBuffer(4 * rows)
+    res = hip.DeviceBuffer(8)
+    sp = stream.handle
+    variants = {
+        "matvec": lambda: dt.matvec(dx.ptr, 1, dl.ptr, sp),
+        "matvec_then_argmax": lambda: (dt.matvec(dx.ptr, 1, dl.ptr, sp),
+                                       qmv.device_greedy_argmax(dl.ptr, rows, res.ptr, sp)),
+        "fused_matvec_argmax": lambda: qmv.device_matvec_argmax(dt, dx.ptr, dl.ptr, res.ptr, sp),
+    }
+    out = {"shape": f"{rows}x{cols} Q6_K", "packed_bytes": nbytes}
+    for name, fn in variants.items():
+        fn()
+        stream.synchronize()
+        g = hip.Graph(stream)
+        g.begin()
+        fn()
+        g.end()
+        g.replay()
+        stream.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        stream.synchronize()
+        us = e0.elapsed_ms(e1) / reps * 1e3
+        out[name + "_us"] = round(us, 2)
+    out["matvec_gbs"] = round(nbytes / (out["matvec_us"] * 1e-6) / 1e9, 1)
+    dt.close()
+    return out
+
+
 def committed_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
     summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by a copy-kernel
@@ -284,6 +326,7 @@ def main():
             extra["m8_set"] = {"ms_per_step": round(r8["ms_per_step"], 4),
                                "weight_gbs": round(total_bytes / (r8["elapsed"] / max(5, args.steps // 5)) / 1e9, 1),
                                "positions_per_s": round(8 / (r8["ms_per_step"] * 1e-3), 1)}
+        extra["vocab_projection"] = vocab_bench(qmv, hip, stream, max(10, args.steps // 2))
         probe = importlib.import_module("my-inference-engine_amd.probe")
         extra["hbm_read_probe"] = probe.read_bandwidth(1 << 30, 512, 10)
         extra["hbm_fraction_of_read_probe"] = round(value / extra["hbm_read_probe"]["gbs"], 4)

@@ -139,6 +139,17 @@ int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count,
                                 const float *d_inputs, int batch_count,
                                 float *const *d_outputs, void *stream);
 
+/*
+ * Vocabulary projection fused with greedy sampling: d_logits[N] = W x for one
+ * position, and in the same launch d_result[0] = the greedy token (largest
+ * logit, lowest id on ties) or -1, d_result[1] = 1 if every logit was finite,
+ * else 0 (the contract of src/sampler.cpp:29-51, whose caller runs after the
+ * output projection, src/qwen2_architecture.cpp:1504-1523). The token is the
+ * argmax of exactly the logits written.
+ */
+int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *d_input,
+                                 float *d_logits, int *d_result, void *stream);
+
 /* Device decode of rows into d_output[row_count, K] (see qmv_dequantize_rows_f32). */
 int qmv_device_dequantize_f32(qmv_device_tensor tensor, int first_row,
                               int row_count, float *d_output, void *stream);

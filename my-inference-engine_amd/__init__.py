@@ -102,6 +102,7 @@ HIP_SIGNATURES = {
     "qmv_set_device": (ctypes.c_int, [ctypes.c_int]),
     "qmv_device_count": (ctypes.c_int, []),
     "qmv_debug_fail_next_calls": (None, [ctypes.c_int]),
+    "qmv_device_matvec_argmax_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
 }
 
@@ -264,6 +265,12 @@ def device_matvec_group(tensors: Sequence[DeviceTensor], d_x: int, batch: int, d
     hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
     outs = (ctypes.c_void_p * n)(*d_outs)
     if not hip_lib().qmv_device_matvec_group_f32(hs, n, d_x, batch, outs, stream):
+        raise QmvError(last_error())
+
+
+def device_matvec_argmax(tensor: "DeviceTensor", d_x: int, d_logits: int, d_result: int, stream: int = 0) -> None:
+    """Fused vocab projection + greedy argmax (M = 1) on device buffers."""
+    if hip_lib().qmv_device_matvec_argmax_f32(tensor.handle, d_x, d_logits, d_result, stream) != 1:
         raise QmvError(last_error())
 
 

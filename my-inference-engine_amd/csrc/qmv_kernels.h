@@ -39,7 +39,18 @@ struct MatvecParams {
     float *partials;
     unsigned *counters; /* all zero between launches */
     int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
+    /* Fused greedy argmax (single tensor, M = 1; result non-null): tile and
+     * group candidates (argmax_words(tiles) words), group and top arrival
+     * counts (argmax_counts(tiles), zero between launches) and the result. */
+    uint64_t *argmax_cand;
+    unsigned *argmax_count;
+    int *argmax_result;
+    int argmax_tiles;
 };
+
+/* Workspace of a fused argmax over `tiles` tiles (groups of 64 tiles). */
+inline size_t argmax_words(size_t tiles) { return tiles + (tiles + 63) / 64; }
+inline size_t argmax_counts(size_t tiles) { return (tiles + 63) / 64 + 1; }
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,

@@ -711,6 +711,109 @@ template <int FMT, int M> struct MatvecOccupancy {
     static constexpr int value = M == 1 ? QMV_WAVES_PER_SIMD_M1 : QMV_WAVES_PER_SIMD_MN;
 };
 
+/* Greedy-argmax merge (src/sampler.cpp:29-51 semantics): the larger value
+ * wins, the lower index on equal values, so any merge order gives the same
+ * winner. */
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2)
+{
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+
+/* Wave-wide argmax of (v, i, bad): every lane ends with the result. */
+__device__ __forceinline__ void wave_argmax(float &v, int &i, int &bad)
+{
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float v2 = __shfl_xor(v, o);
+        const int i2 = __shfl_xor(i, o);
+        bad |= __shfl_xor(bad, o);
+        argmax_merge(v, i, v2, i2);
+    }
+}
+
+/* A tile's argmax candidate as one 64-bit word: value bits, and below the
+ * top bit of the high word the row index, with the top bit set if any row of
+ * the tile was not finite. */
+__device__ __forceinline__ uint64_t pack_candidate(float v, int i, int bad)
+{
+    return (uint64_t)__float_as_uint(v) | ((uint64_t)((uint32_t)i & 0x7fffffffu | (bad ? 0x80000000u : 0u)) << 32);
+}
+
+/* Fused greedy argmax over a single-tensor M = 1 launch, in two levels so
+ * that no counter sees more than QMV_ARGMAX_GROUP arrivals (arrivals at one
+ * address serialise in the memory-side atomic unit): the wave that holds a
+ * tile's final logits reduces them to a candidate, publishes it and counts
+ * it in its group of tiles; the last tile of a group reduces the group's
+ * candidates and counts the group; the last group reduces the group
+ * candidates and writes result[0] = token (or -1) and result[1] = 1 if every
+ * logit was finite. Candidates and counts use agent-scope atomics; each last
+ * arriver resets its counter. */
+#define QMV_ARGMAX_GROUP 64
+
+/* Reduce candidates cand[first .. first + n) (n <= 64), one per lane. */
+__device__ __forceinline__ void reduce_candidates(const uint64_t *cand, int first, int n, int lane, float &v, int &i,
+                                                  int &bad)
+{
+    v = -INFINITY;
+    i = 0x7fffffff;
+    bad = 0;
+    if (lane < n) {
+        const uint64_t c = __hip_atomic_load(cand + first + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t hi = (uint32_t)(c >> 32);
+        bad = (int)(hi >> 31);
+        v = __uint_as_float((uint32_t)c);
+        i = (int)(hi & 0x7fffffffu);
+    }
+    wave_argmax(v, i, bad);
+}
+
+/* Publish a candidate and count it; true for the last of `expected`. */
+__device__ __forceinline__ bool publish_and_count(uint64_t *slot, uint64_t c, unsigned *count, int expected, int lane)
+{
+    if (lane == 0) __hip_atomic_store(slot, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+    if (prev != (unsigned)expected - 1u) return false;
+    if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::: "memory");
+    return true;
+}
+
+/* Workspace: argmax_cand[tiles + groups] (tile candidates, then group
+ * candidates), argmax_count[groups + 1] (group counts, then the top count). */
+__device__ __forceinline__ void tile_argmax(const MatvecParams &p, int tile, bool valid, int row, float y, int lane)
+{
+    const int tiles = p.argmax_tiles;
+    const int groups = (tiles + QMV_ARGMAX_GROUP - 1) / QMV_ARGMAX_GROUP;
+    const bool fin = isfinite(y);
+    float v = valid && fin ? y : -INFINITY;
+    int i = valid && fin ? row : 0x7fffffff;
+    int bad = valid && !fin;
+    wave_argmax(v, i, bad);
+    const int g = tile / QMV_ARGMAX_GROUP;
+    const int first = g * QMV_ARGMAX_GROUP;
+    const int in_group = min(QMV_ARGMAX_GROUP, tiles - first);
+    if (!publish_and_count(p.argmax_cand + tile, pack_candidate(v, i, bad), p.argmax_count + g, in_group, lane))
+        return;
+    reduce_candidates(p.argmax_cand, first, in_group, lane, v, i, bad);
+    if (!publish_and_count(p.argmax_cand + tiles + g, pack_candidate(v, i, bad), p.argmax_count + groups, groups,
+                           lane))
+        return;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff, bb = 0;
+    for (int f = 0; f < groups; f += 64) {
+        reduce_candidates(p.argmax_cand + tiles, f, min(64, groups - f), lane, v, i, bad);
+        bb |= bad;
+        argmax_merge(bv, bi, v, i);
+    }
+    if (lane == 0) {
+        p.argmax_result[0] = bb || bi == 0x7fffffff ? -1 : bi;
+        p.argmax_result[1] = bb ? 0 : 1;
+    }
+}
+
 /* The workgroup's place in a launch: job, tile, K-split, and this wave's
  * K-units [u_begin, u_end). */
 struct WgWork {
@@ -763,6 +866,8 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
 #pragma unroll
             for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = sum[m];
         }
+        if constexpr (M == 1)
+            if (p.argmax_result) tile_argmax(p, w.tile, row < job.rows, row, sum[0], lane);
         return;
     }
 
@@ -776,12 +881,15 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
     prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
     if (prev != (unsigned)job.splits - 1u) return;
     asm volatile("" ::: "memory");
+    float fin[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const float s = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
-        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = s;
+        fin[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
+        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = fin[m];
     }
     if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (M == 1)
+        if (p.argmax_result) tile_argmax(p, w.tile, row < job.rows, row, fin[0], lane);
 }
 
 /* kOne: every wave takes at most one unit (units_per_wave == 1), so no
@@ -1162,10 +1270,6 @@ __global__ void repack_kernel(const uint8_t *__restrict__ raw, uint8_t *__restri
 /* ---- greedy argmax ----------------------------------------------------------
  * Stage 1: each workgroup reduces a chunk to (max, lowest index) and counts
  * non-finite values; stage 2: one workgroup combines in chunk order. */
-__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2)
-{
-    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
-}
 
 __global__ void __launch_bounds__(256)
 argmax_stage1(const float *__restrict__ logits, int n, float *__restrict__ bval, int *__restrict__ bidx,

@@ -149,6 +149,9 @@ struct Workspace {
     int *arg_idx = nullptr;
     int *arg_bad = nullptr;
     int *arg_result = nullptr; /* 2 ints */
+    uint64_t *fused_cand = nullptr;  /* fused argmax: tile and group candidates */
+    unsigned *fused_count = nullptr; /* fused argmax: arrival counts, zero between launches */
+    size_t fused_cap = 0;            /* tiles */
     std::mutex mu;
 };
 
@@ -185,6 +188,30 @@ int workspace_reserve(Workspace &ws, hipStream_t stream, size_t partials, size_t
 }
 
 constexpr int kArgBlocks = 512;
+
+/* Candidate slots and counters for a fused argmax over `tiles` tiles (grown
+ * outside graph capture only; counters are zeroed on the launch stream). */
+int workspace_fused_argmax(Workspace &ws, hipStream_t stream, size_t tiles)
+{
+    if (tiles <= ws.fused_cap) return 1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+        set_error("workspace must grow during stream capture; run the call once before capturing");
+        return 0;
+    }
+    HIP_TRY(hipStreamSynchronize(stream));
+    const size_t n = tiles + tiles / 2 + 256;
+    if (ws.fused_cand) HIP_TRY(hipFree(ws.fused_cand));
+    if (ws.fused_count) HIP_TRY(hipFree(ws.fused_count));
+    ws.fused_cand = nullptr;
+    ws.fused_count = nullptr;
+    ws.fused_cap = 0;
+    HIP_TRY(hipMalloc(&ws.fused_cand, qmv::argmax_words(n) * sizeof(uint64_t)));
+    HIP_TRY(hipMalloc(&ws.fused_count, qmv::argmax_counts(n) * sizeof(unsigned)));
+    HIP_TRY(hipMemsetAsync(ws.fused_count, 0, qmv::argmax_counts(n) * sizeof(unsigned), stream));
+    ws.fused_cap = n;
+    return 1;
+}
 
 int workspace_argmax(Workspace &ws)
 {
@@ -435,9 +462,11 @@ Plan plan_for(long long total_tiles, int units)
     return p;
 }
 
-/* Enqueue one launch over `count` tensors sharing the input. */
+/* Enqueue one launch over `count` tensors sharing the input; with d_argmax
+ * (one tensor, batch 1) the launch also writes the greedy argmax of its
+ * outputs there. */
 int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
-                 hipStream_t stream, Workspace &ws)
+                 hipStream_t stream, Workspace &ws, int *d_argmax = nullptr)
 {
     const QmvDeviceTensor *t0 = ts[0];
     long long total_tiles = 0;
@@ -481,6 +510,17 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (!workspace_reserve(ws, stream, partials, counters)) return 0;
     p.partials = ws.partials;
     p.counters = ws.counters;
+    if (d_argmax) {
+        if (count != 1 || batch != 1) {
+            set_error("fused argmax takes one tensor and one position");
+            return 0;
+        }
+        if (!workspace_fused_argmax(ws, stream, (size_t)t0->tiles)) return 0;
+        p.argmax_cand = ws.fused_cand;
+        p.argmax_count = ws.fused_count;
+        p.argmax_result = d_argmax;
+        p.argmax_tiles = t0->tiles;
+    }
     HIP_TRY(qmv::launch_matvec(t0->geo.format, p, batch, (int)wg, plan.waves, stream));
     return 1;
 }
@@ -709,6 +749,19 @@ QMV_API int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_input
                                   float *d_outputs, void *stream)
 {
     return qmv_device_matvec_group_f32(&tensor, 1, d_inputs, batch_count, &d_outputs, stream);
+}
+
+QMV_API int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *d_input, float *d_logits,
+                                         int *d_result, void *stream)
+{
+    if (tensor == nullptr || d_input == nullptr || d_logits == nullptr || d_result == nullptr) {
+        set_error("invalid fused argmax arguments");
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(tensor->device));
+    hipStream_t s = (hipStream_t)stream;
+    Workspace &ws = workspace_for(tensor->device, s);
+    return launch_group(&tensor, 1, d_input, 1, &d_logits, s, ws, d_result);
 }
 
 QMV_API int qmv_device_dequantize_f32(qmv_device_tensor t, int first_row, int row_count, float *d_output,

@@ -109,6 +109,7 @@ def test_invalid_sampler_and_device_args_fail_without_gpu(qmv):
     assert lib.qmv_greedy_sample_f32(x.ctypes.data, 0, ctypes.byref(tok)) == 0 and tok.value == -1
     assert lib.qmv_device_matvec_f32(None, None, 1, None, None) == 0
     assert lib.qmv_device_greedy_argmax_f32(None, 10, None, None) == 0
+    assert lib.qmv_device_matvec_argmax_f32(None, None, None, None, None) == 0
     assert lib.qmv_device_tensor_create(None, None) == 0
     assert lib.qmv_dequantize_rows_f32(None, 0, 1, x.ctypes.data) == 0
 

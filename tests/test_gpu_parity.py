@@ -457,3 +457,82 @@ def test_device_argmax(qmv, gpu, hip):
     qmv.device_greedy_argmax(dx.ptr, x.size, res.ptr, stream.handle)
     stream.synchronize()
     assert res.to_array(np.int32, (2,)).tolist() == [10, 1]
+
+
+# ---- vocabulary projection fused with greedy sampling ----------------------------
+
+def _fused(qmv, hip, raw, t, rows, cols, x, reps=1, graph=False):
+    dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+    dx = hip.DeviceBuffer.from_array(x)
+    dl = hip.DeviceBuffer(4 * rows)
+    dref = hip.DeviceBuffer(4 * rows)
+    res = hip.DeviceBuffer(8)
+    stream = hip.Stream()
+    dt.matvec(dx.ptr, 1, dref.ptr, stream.handle)
+    outs = []
+    g = None
+    if graph:
+        qmv.device_matvec_argmax(dt, dx.ptr, dl.ptr, res.ptr, stream.handle)  # sizes the workspace
+        stream.synchronize()
+        g = hip.Graph(stream)
+        g.begin()
+        qmv.device_matvec_argmax(dt, dx.ptr, dl.ptr, res.ptr, stream.handle)
+        g.end()
+    for _ in range(reps):
+        res.fill(0x55)
+        if g is not None:
+            g.replay()
+        else:
+            qmv.device_matvec_argmax(dt, dx.ptr, dl.ptr, res.ptr, stream.handle)
+        stream.synchronize()
+        outs.append(res.to_array(np.int32, (2,)).tolist())
+    logits = dl.to_array(np.float32, (rows,))
+    ref = dref.to_array(np.float32, (rows,))
+    dt.close()
+    return outs, logits, ref
+
+
+@pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 1000, 3584), (B.Q6_K, 4864, 896 * 4), (B.Q8_0, 130, 896),
+                                         (B.Q5_0, 64, 1536), (B.Q6_K, 7, 18944)])
+def test_fused_argmax_matches_its_logits(qmv, oracle, gpu, hip, t, rows, cols):
+    """The fused launch writes the same logits as the plain matvec (bit for
+    bit) and returns the lowest-index argmax of exactly those logits; the
+    logits are within tolerance of the oracle."""
+    raw = qmv.synth_tensor(t, rows, cols, seed=rows)
+    x = qmv.synth_normal(cols, seed=cols)
+    outs, logits, ref = _fused(qmv, hip, raw, t, rows, cols, x, reps=3)
+    assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32))
+    expect = int(np.argmax(logits))
+    assert all(o == [expect, 1] for o in outs), (outs, expect)
+    y_ref = oracle.matvec(raw, t, rows, cols, x)
+    _, absdot = oracle.row_stats(raw, t, rows, cols, x)
+    check_rows(logits, y_ref, absdot, "fused argmax logits")
+
+
+def test_fused_argmax_vocab_shape_and_graph(qmv, gpu, hip):
+    """Vocabulary shape (151936 x 3584 Q6_K): eager and graph-replayed fused
+    launches agree with the argmax of their logits on every replay."""
+    t, rows, cols = B.Q6_K, 151936, 3584
+    raw = qmv.synth_tensor(t, rows, cols, seed=44)
+    x = qmv.synth_normal(cols, seed=45)
+    outs, logits, ref = _fused(qmv, hip, raw, t, rows, cols, x, reps=4, graph=True)
+    assert np.array_equal(logits.view(np.uint32), ref.view(np.uint32))
+    expect = int(np.argmax(logits))
+    assert all(o == [expect, 1] for o in outs), (outs, expect)
+
+
+def test_fused_argmax_ties_and_non_finite(qmv, gpu, hip):
+    """All-zero input: every logit ties at 0 and the lowest id wins. A row
+    with an infinite scale makes its logit non-finite: token -1, flag 0, as
+    the reference sampler rejects non-finite logits."""
+    t, rows, cols = B.Q8_0, 300, 256
+    raw = qmv.synth_tensor(t, rows, cols, seed=9)
+    outs, logits, _ = _fused(qmv, hip, raw, t, rows, cols, np.zeros(cols, dtype=np.float32))
+    assert outs == [[0, 1]] and not logits.any()
+    bad = raw.copy()
+    bpr = cols // 32
+    bad[(200 * bpr) * 34:(200 * bpr) * 34 + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), dtype=np.uint8)
+    x = qmv.synth_normal(cols, seed=10)
+    outs, logits, _ = _fused(qmv, hip, bad, t, rows, cols, x)
+    assert not np.isfinite(logits[200])
+    assert outs == [[-1, 0]]
