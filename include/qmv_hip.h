@@ -150,6 +150,17 @@ int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count,
 int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *d_input,
                                  float *d_logits, int *d_result, void *stream);
 
+/*
+ * Embedding lookup: d_output[i, K] = row d_token_ids[i] of the tensor decoded
+ * to fp32 (i < count <= 65535), bit-identical to the reference's per-row
+ * decode qwen2_decode_quantized_embedding_row (src/qwen2_architecture.cpp:
+ * 375-456) for each id. The ids are read on the device (for example the token
+ * just written by qmv_device_matvec_argmax_f32); an id outside [0, N) cannot
+ * be rejected there and fills its output row with NaN instead.
+ */
+int qmv_device_embed_rows_f32(qmv_device_tensor tensor, const int *d_token_ids,
+                              int count, float *d_output, void *stream);
+
 /* Device decode of rows into d_output[row_count, K] (see qmv_dequantize_rows_f32). */
 int qmv_device_dequantize_f32(qmv_device_tensor tensor, int first_row,
                               int row_count, float *d_output, void *stream);

@@ -1227,6 +1227,45 @@ dequant_kernel(const uint8_t *__restrict__ w, float *__restrict__ out, int rows,
     }
 }
 
+/* ---- embedding-row gather -----------------------------------------------------
+ * out[i * cols + k] = row ids[i] of the tensor, decoded exactly like
+ * dequant_kernel (bit-identical to the block decoders). One lane per
+ * (position i, K-unit); the row's bytes of a unit sit at lane id % 64 of its
+ * slab. An id outside [0, rows) fills its output row with NaN (ids live in
+ * device memory, so the host cannot check them). */
+template <int FMT>
+__global__ void __launch_bounds__(64)
+gather_rows_kernel(const uint8_t *__restrict__ w, const int *__restrict__ ids, float *__restrict__ out, int rows,
+                   int cols, int units)
+{
+    using Unit = typename UnitOf<FMT>::T;
+    constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    constexpr int UW = UnitOf<FMT>::kWeights;
+    const int i = blockIdx.y;
+    const int unit = blockIdx.x * 64 + threadIdx.x;
+    if (unit >= units) return;
+    const int id = ids[i];
+    float *dst = out + (size_t)i * cols + (size_t)unit * UW;
+    const int kleft = cols - unit * UW;
+    if (id < 0 || id >= rows) {
+        for (int k = 0; k < UW && k < kleft; ++k) dst[k] = __builtin_nanf("");
+        return;
+    }
+    Unit u;
+    load_unit(u, w + ((size_t)(id >> 6) * units + unit) * SLAB, id & 63);
+    const UnitScales<FMT> s = unit_scales<FMT>(u);
+#pragma unroll
+    for (int r = 0; r < RegionCount<FMT>::value; ++r) {
+        float v[8];
+        region_w<FMT, true>(u, s, r, v, 0.0f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = region_k<FMT>(r, e);
+            if (UW == 256 || k < kleft) dst[k] = v[e];
+        }
+    }
+}
+
 /* ---- upload repack ----------------------------------------------------------
  * Thread per (tile, unit, lane, block-in-unit): copies one packed block from
  * the row-major GGUF bytes into its planes. */
@@ -1383,6 +1422,20 @@ hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int c
     case QMV_FMT_Q6_K: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q6_K>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
     case QMV_FMT_Q8_0: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q8_0>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
     case QMV_FMT_Q5_0: hipLaunchKernelGGL(dequant_kernel<QMV_FMT_Q5_0>, grid, dim3(64), 0, s, w, out, rows, cols, units, first_row, row_count); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, float *out, int rows, int cols,
+                         int units, hipStream_t s)
+{
+    const dim3 grid((units + 63) / 64, count);
+    switch (fmt) {
+    case QMV_FMT_Q4_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q4_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
+    case QMV_FMT_Q6_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q6_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
+    case QMV_FMT_Q8_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q8_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
+    case QMV_FMT_Q5_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q5_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

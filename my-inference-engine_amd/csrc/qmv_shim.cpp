@@ -764,6 +764,19 @@ QMV_API int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *
     return launch_group(&tensor, 1, d_input, 1, &d_logits, s, ws, d_result);
 }
 
+QMV_API int qmv_device_embed_rows_f32(qmv_device_tensor t, const int *d_token_ids, int count, float *d_output,
+                                      void *stream)
+{
+    if (t == nullptr || d_token_ids == nullptr || d_output == nullptr || count <= 0 || count > 65535) {
+        set_error("invalid embedding gather arguments");
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(t->device));
+    HIP_TRY(qmv::launch_gather(t->geo.format, t->data, d_token_ids, count, d_output, t->rows, t->cols, t->units,
+                               (hipStream_t)stream));
+    return 1;
+}
+
 QMV_API int qmv_device_dequantize_f32(qmv_device_tensor t, int first_row, int row_count, float *d_output,
                                       void *stream)
 {

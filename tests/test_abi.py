@@ -110,6 +110,7 @@ def test_invalid_sampler_and_device_args_fail_without_gpu(qmv):
     assert lib.qmv_device_matvec_f32(None, None, 1, None, None) == 0
     assert lib.qmv_device_greedy_argmax_f32(None, 10, None, None) == 0
     assert lib.qmv_device_matvec_argmax_f32(None, None, None, None, None) == 0
+    assert lib.qmv_device_embed_rows_f32(None, None, 1, None, None) == 0
     assert lib.qmv_device_tensor_create(None, None) == 0
     assert lib.qmv_dequantize_rows_f32(None, 0, 1, x.ctypes.data) == 0
 

@@ -536,3 +536,31 @@ def test_fused_argmax_ties_and_non_finite(qmv, gpu, hip):
     outs, logits, _ = _fused(qmv, hip, bad, t, rows, cols, x)
     assert not np.isfinite(logits[200])
     assert outs == [[-1, 0]]
+
+
+# ---- embedding rows gathered by device token ids ------------------------------------
+
+@pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 1000, 1536), (B.Q6_K, 130, 896 * 4), (B.Q8_0, 151, 7 * 32 + 512),
+                                         (B.Q5_0, 64, 1536)])
+def test_embed_rows_bit_exact(qmv, oracle, gpu, hip, t, rows, cols):
+    """Gathered rows (duplicates, first and last rows, rows of the partial last
+    tile) equal the oracle's decode bit for bit; an out-of-range id gives a
+    NaN row and leaves the others exact."""
+    raw = qmv.synth_tensor(t, rows, cols, seed=rows + 3)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+    ids = np.array([0, rows - 1, 5, 5, rows // 2, rows - 2, 63 % rows, rows, -1, 1], dtype=np.int32)
+    d_ids = hip.DeviceBuffer.from_array(ids)
+    out = hip.DeviceBuffer(4 * ids.size * cols)
+    stream = hip.Stream()
+    qmv.device_embed_rows(dt, d_ids.ptr, ids.size, out.ptr, stream.handle)
+    stream.synchronize()
+    got = out.to_array(np.float32, (ids.size, cols))
+    for i, r in enumerate(ids.tolist()):
+        if 0 <= r < rows:
+            exp = oracle.dequantize_rows(raw, t, rows, cols, r, 1)[0]
+            nan = np.isnan(exp)
+            assert np.array_equal(np.isnan(got[i]), nan)
+            assert np.array_equal(got[i][~nan].view(np.uint32), exp[~nan].view(np.uint32)), (i, r)
+        else:
+            assert np.isnan(got[i]).all(), (i, r)
+    dt.close()
