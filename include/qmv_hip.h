@@ -140,6 +140,37 @@ int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count,
                                 float *const *d_outputs, void *stream);
 
 /*
+ * Grouped matvec with an addend fused into the store: for each tensor i,
+ * d_outputs[i][b*N_i + r] = (W_i x_b)[r] + d_addends[i][b*addend_strides[i] + r]
+ * (the fp32 sum of the row result and the addend, as the reference's separate
+ * tensor_add_f32, src/tensor.cpp:5-23, computes it). addend_strides[i] = 0
+ * adds one vector to every position: the q/k/v biases of
+ * qwen2_layer_project / _project_batch (src/qwen2_architecture.cpp:714-733,
+ * 763-807). addend_strides[i] = N_i with d_addends[i] == d_outputs[i] adds
+ * the residual in place: x += W h after the attention output and FFN down
+ * projections (src/qwen2_architecture.cpp:1363-1374, 1450-1463). A null
+ * d_addends[i] stores the plain product. Other overlaps of an addend with an
+ * output are rejected. Stride otherwise >= N_i.
+ */
+int qmv_device_matvec_add_group_f32(const qmv_device_tensor *tensors, int count,
+                                    const float *d_inputs, int batch_count,
+                                    const float *const *d_addends,
+                                    const int *addend_strides,
+                                    float *const *d_outputs, void *stream);
+
+/*
+ * FFN gate and up projections of one shared input fused with SwiGLU:
+ * d_outputs[b*N + r] = up_b[r] * silu(gate_b[r]), silu(g) = g / (1 + exp(-g)),
+ * the element rule of transformer_swiglu_f32 (src/transformer_ops.cpp:163-
+ * 176) applied to the two projections (src/qwen2_architecture.cpp:1399-1434).
+ * One launch; neither projection is stored. gate and up share type, shape
+ * and device.
+ */
+int qmv_device_matvec_swiglu_f32(qmv_device_tensor gate, qmv_device_tensor up,
+                                 const float *d_inputs, int batch_count,
+                                 float *d_outputs, void *stream);
+
+/*
  * Vocabulary projection fused with greedy sampling: d_logits[N] = W x for one
  * position, and in the same launch d_result[0] = the greedy token (largest
  * logit, lowest id on ties) or -1, d_result[1] = 1 if every logit was finite,
@@ -164,6 +195,21 @@ int qmv_device_embed_rows_f32(qmv_device_tensor tensor, const int *d_token_ids,
 /* Device decode of rows into d_output[row_count, K] (see qmv_dequantize_rows_f32). */
 int qmv_device_dequantize_f32(qmv_device_tensor tensor, int first_row,
                               int row_count, float *d_output, void *stream);
+
+/*
+ * RMSNorm of batch_count device vectors of length elements each:
+ * d_output[b*L + i] = (x[i] / sqrt(mean(x^2) + epsilon)) * d_weight[i] with
+ * x = d_input + b*L, the contract of tensor_rms_norm_f32 (src/tensor.cpp:
+ * 99-136; the decode step's attention and FFN norms, src/qwen2_architecture.
+ * cpp:1241-1260, 1376-1397, and the output norm). Same argument rules: null
+ * pointers, length <= 0 or epsilon <= 0 fail. The sum of squares is taken
+ * in a fixed parallel order, so it differs from the reference's sequential
+ * sum in the last bits (well inside 2e-5 relative). d_output may be d_input
+ * itself; other overlaps fail.
+ */
+int qmv_device_rms_norm_f32(const float *d_input, const float *d_weight,
+                            int length, int batch_count, float epsilon,
+                            float *d_output, void *stream);
 
 /*
  * Greedy argmax over device logits. Writes d_result[0] = token id (or -1)

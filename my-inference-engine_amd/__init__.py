@@ -105,6 +105,11 @@ HIP_SIGNATURES = {
     "qmv_device_matvec_argmax_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "qmv_device_embed_rows_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
     "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qmv_device_matvec_add_group_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, ctypes.c_int,
+                                                       ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int),
+                                                       ctypes.POINTER(_vp), _vp]),
+    "qmv_device_matvec_swiglu_f32": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _vp, _vp]),
+    "qmv_device_rms_norm_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float, _vp, _vp]),
 }
 
 SYNTH_SIGNATURES = {
@@ -266,6 +271,33 @@ def device_matvec_group(tensors: Sequence[DeviceTensor], d_x: int, batch: int, d
     hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
     outs = (ctypes.c_void_p * n)(*d_outs)
     if not hip_lib().qmv_device_matvec_group_f32(hs, n, d_x, batch, outs, stream):
+        raise QmvError(last_error())
+
+
+def device_matvec_add_group(tensors: Sequence[DeviceTensor], d_x: int, batch: int, d_adds: Sequence[int],
+                            add_strides: Sequence[int], d_outs: Sequence[int], stream: int = 0) -> None:
+    """Grouped matvec with y_i += add_i fused (stride 0: a bias for every
+    position; stride N_i with add_i == y_i: a residual added in place; a 0
+    address: no addend)."""
+    n = len(tensors)
+    hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
+    adds = (ctypes.c_void_p * n)(*[a or None for a in d_adds])
+    lds = (ctypes.c_int * n)(*add_strides)
+    outs = (ctypes.c_void_p * n)(*d_outs)
+    if not hip_lib().qmv_device_matvec_add_group_f32(hs, n, d_x, batch, adds, lds, outs, stream):
+        raise QmvError(last_error())
+
+
+def device_matvec_swiglu(gate: DeviceTensor, up: DeviceTensor, d_x: int, batch: int, d_out: int,
+                         stream: int = 0) -> None:
+    """d_out[b, r] = up(x_b)[r] * silu(gate(x_b)[r]) in one launch."""
+    if not hip_lib().qmv_device_matvec_swiglu_f32(gate.handle, up.handle, d_x, batch, d_out, stream):
+        raise QmvError(last_error())
+
+
+def device_rms_norm(d_x: int, d_weight: int, length: int, batch: int, epsilon: float, d_out: int,
+                    stream: int = 0) -> None:
+    if not hip_lib().qmv_device_rms_norm_f32(d_x, d_weight, length, batch, epsilon, d_out, stream):
         raise QmvError(last_error())
 
 

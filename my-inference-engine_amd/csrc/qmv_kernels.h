@@ -26,6 +26,8 @@ struct MatvecJob {
     int wg_begin;        /* first workgroup id of this job in the grid */
     int partial_offset;  /* float offset of this job's partials in the workspace */
     int counter_offset;  /* offset of this job's per-tile arrival counters */
+    const float *add;    /* optional: y[m * ldy + row] += add[m * ldadd + row] */
+    int ldadd;           /* 0: one vector for every position (a bias) */
 };
 
 struct MatvecParams {
@@ -46,6 +48,13 @@ struct MatvecParams {
     unsigned *argmax_count;
     int *argmax_result;
     int argmax_tiles;
+    /* Fused SwiGLU (swiglu != 0; jobs 0 = gate and 1 = up, equal rows):
+     * job 0's y receives up * silu(gate) and neither projection is stored.
+     * Each tile's final values are published to pair_vals[2][tiles][M][64]
+     * and counted in pair_count[tiles] (zero between launches). */
+    int swiglu;
+    float *pair_vals;
+    unsigned *pair_count;
 };
 
 /* Workspace of a fused argmax over `tiles` tiles (groups of 64 tiles). */
@@ -60,6 +69,8 @@ hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, f
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
                          int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
                          hipStream_t s);
+hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out,
+                           hipStream_t s);
 hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,
                          int *result, hipStream_t s);
 

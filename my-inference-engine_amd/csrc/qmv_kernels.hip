@@ -837,9 +837,71 @@ __device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave)
     return w;
 }
 
+/* silu(g) * u, as src/transformer_ops.cpp:163-176 computes each element
+ * (x / (1 + exp(-x)), then the product with up). */
+__device__ __forceinline__ float swiglu_value(float g, float u)
+{
+    return u * (g / (1.0f + expf(-g)));
+}
+
+/* Fused SwiGLU: publish this tile's final gate or up values and count the
+ * tile; the second of the pair to arrive reads the other's values and writes
+ * up * silu(gate) to job 0's output, then resets the count. */
+template <int M>
+__device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork &w, int lane, int row, bool valid,
+                                            const float (&v)[M])
+{
+    const MatvecJob &out = p.job[0];
+    float *mine = p.pair_vals + ((size_t)w.job * out.tiles + w.tile) * M * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < M; ++m) store_partial(mine + m * 64, v[m]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(p.pair_count + w.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+    if (prev == 0u) return;
+    asm volatile("" ::: "memory");
+    const float *other = p.pair_vals + ((size_t)(1 - w.job) * out.tiles + w.tile) * M * 64 + lane;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float o = load_partial(other + m * 64);
+        const float g = w.job == 0 ? v[m] : o;
+        const float u = w.job == 0 ? o : v[m];
+        if (valid) out.y[(size_t)m * out.ldy + row] = swiglu_value(g, u);
+    }
+    if (lane == 0) __hip_atomic_store(p.pair_count + w.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* A tile's final row values v[m] (lane = row within the tile): add the
+ * job's addend, then store them, or hand them to the fused SwiGLU, and feed
+ * the fused argmax. The addend is read and the output written by the same
+ * lane, so an addend that is the output itself (a residual added in place)
+ * is safe. */
+template <int M>
+__device__ __forceinline__ void emit_tile(const MatvecParams &p, const WgWork &w, int lane, float (&v)[M])
+{
+    const MatvecJob &job = p.job[w.job];
+    const int row = w.tile * 64 + lane;
+    const bool valid = row < job.rows;
+    if (job.add != nullptr && valid) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) v[m] += job.add[(size_t)m * job.ldadd + row];
+    }
+    if (p.swiglu) {
+        swiglu_pair<M>(p, w, lane, row, valid, v);
+        return;
+    }
+    if (valid) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = v[m];
+    }
+    if constexpr (M == 1)
+        if (p.argmax_result) tile_argmax(p, w.tile, valid, row, v[0], lane);
+}
+
 /* After every wave has written red[wave][m][row] (row = tile row 0..63) and
  * the workgroup has synchronised, wave 0 adds the waves in wave order and
- * stores the rows, or, for a tile split along K, publishes this split's
+ * emits the rows, or, for a tile split along K, publishes this split's
  * partial; the last split to arrive adds all partials of the tile in split
  * order (a fixed order, so results do not depend on arrival order).
  * Partials and counters are accessed only with agent-scope atomics, which are
@@ -859,15 +921,9 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
         for (int v = 1; v < nwaves; ++v) s += red[v][m][lane];
         sum[m] = s;
     }
-    const int row = w.tile * 64 + lane;
 
     if (job.splits == 1) {
-        if (row < job.rows) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = sum[m];
-        }
-        if constexpr (M == 1)
-            if (p.argmax_result) tile_argmax(p, w.tile, row < job.rows, row, sum[0], lane);
+        emit_tile<M>(p, w, lane, sum);
         return;
     }
 
@@ -883,13 +939,9 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
     asm volatile("" ::: "memory");
     float fin[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        fin[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
-        if (row < job.rows) job.y[(size_t)m * job.ldy + row] = fin[m];
-    }
+    for (int m = 0; m < M; ++m) fin[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
     if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if constexpr (M == 1)
-        if (p.argmax_result) tile_argmax(p, w.tile, row < job.rows, row, fin[0], lane);
+    emit_tile<M>(p, w, lane, fin);
 }
 
 /* kOne: every wave takes at most one unit (units_per_wave == 1), so no
@@ -1366,6 +1418,32 @@ argmax_stage2(const float *__restrict__ bval, const int *__restrict__ bidx, cons
     result[1] = bad ? 0 : 1;
 }
 
+/* RMSNorm (tensor_rms_norm_f32, src/tensor.cpp:99-136) of one vector per
+ * workgroup: out = (x / sqrt(mean(x^2) + eps)) * w. The sum of squares runs
+ * in a fixed order (each thread strides the vector, then a butterfly within
+ * the wave and the four wave sums in order), so results are deterministic;
+ * the division and square root are IEEE-rounded. Every thread reads the
+ * elements it writes after the workgroup barrier, so out may be x itself. */
+#define QMV_NORM_THREADS 256
+__global__ void __launch_bounds__(QMV_NORM_THREADS)
+rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, float *out)
+{
+    const float *xv = x + (size_t)blockIdx.x * n;
+    float *ov = out + (size_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += QMV_NORM_THREADS) s += xv[i] * xv[i];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+    __shared__ float wave_sum[QMV_NORM_THREADS / 64];
+    if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float total = wave_sum[0];
+#pragma unroll
+    for (int v = 1; v < QMV_NORM_THREADS / 64; ++v) total += wave_sum[v];
+    const float denom = sqrtf(total / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += QMV_NORM_THREADS) ov[i] = (xv[i] / denom) * w[i];
+}
+
 /* ---- host-side launchers -------------------------------------------------- */
 
 template <int FMT, int M>
@@ -1461,6 +1539,12 @@ hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, s, bval, bidx, bbad, nblocks, result);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out, hipStream_t s)
+{
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(batch), dim3(QMV_NORM_THREADS), 0, s, x, w, n, eps, out);
     return hipGetLastError();
 }
 

@@ -462,11 +462,17 @@ Plan plan_for(long long total_tiles, int units)
     return p;
 }
 
-/* Enqueue one launch over `count` tensors sharing the input; with d_argmax
- * (one tensor, batch 1) the launch also writes the greedy argmax of its
- * outputs there. */
+/* What a launch does with each tile's final rows besides storing them. */
+struct Epilogue {
+    const float *const *add = nullptr; /* per tensor (entries may be null): y += add */
+    const int *ldadd = nullptr;        /* per tensor: 0 = one vector for all positions */
+    int *argmax = nullptr;             /* one tensor, batch 1: greedy argmax of y here */
+    bool swiglu = false;               /* tensors (gate, up): out[0] = up * silu(gate) */
+};
+
+/* Enqueue one launch over `count` tensors sharing the input. */
 int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
-                 hipStream_t stream, Workspace &ws, int *d_argmax = nullptr)
+                 hipStream_t stream, Workspace &ws, const Epilogue &epi = Epilogue())
 {
     const QmvDeviceTensor *t0 = ts[0];
     long long total_tiles = 0;
@@ -495,11 +501,27 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         j.wg_begin = (int)wg;
         j.partial_offset = (int)partials;
         j.counter_offset = (int)counters;
+        if (epi.add && epi.add[i]) {
+            j.add = epi.add[i];
+            j.ldadd = epi.ldadd[i];
+        }
         if (plan.splits > 1) {
             partials += (size_t)ts[i]->tiles * plan.splits * batch * 64;
             counters += (size_t)ts[i]->tiles;
         }
         wg += (long long)ts[i]->tiles * plan.splits;
+    }
+    /* Fused SwiGLU: both projections' final tiles, then one count per tile
+     * pair, after the split-K partials and counters. */
+    const size_t pair_vals = partials, pair_count = counters;
+    if (epi.swiglu) {
+        if (count != 2 || ts[0]->rows != ts[1]->rows) {
+            set_error("fused SwiGLU takes two tensors (gate, up) with equal rows");
+            return 0;
+        }
+        partials += (size_t)2 * t0->tiles * batch * 64;
+        counters += (size_t)t0->tiles;
+        p.swiglu = 1;
     }
     if (wg > INT_MAX || partials > (size_t)INT_MAX || counters > (size_t)INT_MAX) {
         set_error("launch too large");
@@ -510,15 +532,19 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (!workspace_reserve(ws, stream, partials, counters)) return 0;
     p.partials = ws.partials;
     p.counters = ws.counters;
-    if (d_argmax) {
-        if (count != 1 || batch != 1) {
+    if (epi.swiglu) {
+        p.pair_vals = ws.partials + pair_vals;
+        p.pair_count = ws.counters + pair_count;
+    }
+    if (epi.argmax) {
+        if (count != 1 || batch != 1 || epi.swiglu) {
             set_error("fused argmax takes one tensor and one position");
             return 0;
         }
         if (!workspace_fused_argmax(ws, stream, (size_t)t0->tiles)) return 0;
         p.argmax_cand = ws.fused_cand;
         p.argmax_count = ws.fused_count;
-        p.argmax_result = d_argmax;
+        p.argmax_result = epi.argmax;
         p.argmax_tiles = t0->tiles;
     }
     HIP_TRY(qmv::launch_matvec(t0->geo.format, p, batch, (int)wg, plan.waves, stream));
@@ -636,6 +662,34 @@ QMV_API int qmv_dequantize_rows_f32(const QmvTensorView *matrix, int first_row, 
     return 1;
 }
 
+/* Address ranges of device buffers, for the no-overlap rules. */
+static bool overlap(const void *a, size_t abytes, const void *b, size_t bbytes)
+{
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+QMV_API int qmv_device_rms_norm_f32(const float *d_input, const float *d_weight, int length, int batch_count,
+                                    float epsilon, float *d_output, void *stream)
+{
+    /* src/tensor.cpp:116-122: null pointers, length <= 0 and epsilon <= 0
+     * fail (so a NaN epsilon is accepted, as there). */
+    if (d_input == nullptr || d_weight == nullptr || d_output == nullptr || length <= 0 || batch_count <= 0 ||
+        epsilon <= 0) {
+        set_error("invalid RMSNorm arguments");
+        return 0;
+    }
+    const size_t bytes = (size_t)batch_count * length * sizeof(float);
+    if ((d_output != d_input && overlap(d_output, bytes, d_input, bytes)) ||
+        overlap(d_output, bytes, d_weight, (size_t)length * sizeof(float))) {
+        set_error("RMSNorm output overlaps the weight or part of the input");
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(g_device.load()));
+    HIP_TRY(qmv::launch_rms_norm(d_input, d_weight, length, batch_count, epsilon, d_output, (hipStream_t)stream));
+    return 1;
+}
+
 QMV_API int qmv_device_greedy_argmax_f32(const float *d_logits, int vocab_size, int *d_result, void *stream)
 {
     if (d_logits == nullptr || d_result == nullptr || vocab_size <= 0) {
@@ -719,8 +773,11 @@ QMV_API int qmv_device_tensor_info(qmv_device_tensor t, int *rows, int *columns,
     return 1;
 }
 
-QMV_API int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count, const float *d_inputs,
-                                        int batch_count, float *const *d_outputs, void *stream)
+/* Shared checks of the grouped device matvec: same type, column count and
+ * device; outputs overlap neither the input nor each other (every workgroup
+ * reads the whole input while others write their rows). */
+static int group_args_ok(const qmv_device_tensor *tensors, int count, const float *d_inputs, int batch_count,
+                         float *const *d_outputs)
 {
     if (tensors == nullptr || d_inputs == nullptr || d_outputs == nullptr || count <= 0 ||
         count > QMV_MAX_GROUP || batch_count <= 0 || batch_count > QMV_MAX_BATCH) {
@@ -738,6 +795,26 @@ QMV_API int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int co
             return 0;
         }
     }
+    const size_t in_bytes = (size_t)batch_count * tensors[0]->cols * sizeof(float);
+    for (int i = 0; i < count; ++i) {
+        const size_t out_bytes = (size_t)batch_count * tensors[i]->rows * sizeof(float);
+        if (overlap(d_outputs[i], out_bytes, d_inputs, in_bytes)) {
+            set_error("output overlaps the input");
+            return 0;
+        }
+        for (int j = 0; j < i; ++j)
+            if (overlap(d_outputs[i], out_bytes, d_outputs[j], (size_t)batch_count * tensors[j]->rows * 4)) {
+                set_error("outputs overlap each other");
+                return 0;
+            }
+    }
+    return 1;
+}
+
+QMV_API int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count, const float *d_inputs,
+                                        int batch_count, float *const *d_outputs, void *stream)
+{
+    if (!group_args_ok(tensors, count, d_inputs, batch_count, d_outputs)) return 0;
     HIP_TRY(hipSetDevice(tensors[0]->device));
     hipStream_t s = (hipStream_t)stream;
     Workspace &ws = workspace_for(tensors[0]->device, s);
@@ -751,6 +828,65 @@ QMV_API int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_input
     return qmv_device_matvec_group_f32(&tensor, 1, d_inputs, batch_count, &d_outputs, stream);
 }
 
+QMV_API int qmv_device_matvec_add_group_f32(const qmv_device_tensor *tensors, int count, const float *d_inputs,
+                                            int batch_count, const float *const *d_addends,
+                                            const int *addend_strides, float *const *d_outputs, void *stream)
+{
+    if (!group_args_ok(tensors, count, d_inputs, batch_count, d_outputs)) return 0;
+    if (d_addends == nullptr || addend_strides == nullptr) {
+        set_error("invalid addend arguments");
+        return 0;
+    }
+    for (int i = 0; i < count; ++i) {
+        if (d_addends[i] == nullptr) continue;
+        const int n = tensors[i]->rows, ld = addend_strides[i];
+        if (ld != 0 && ld < n) {
+            set_error("addend stride must be 0 or at least the row count");
+            return 0;
+        }
+        const size_t add_bytes = ((size_t)(batch_count - 1) * ld + n) * sizeof(float);
+        const bool in_place = d_addends[i] == d_outputs[i] && ld == n;
+        for (int j = 0; j < count; ++j) {
+            if (j == i && in_place) continue;
+            if (overlap(d_addends[i], add_bytes, d_outputs[j], (size_t)batch_count * tensors[j]->rows * 4)) {
+                set_error("addend overlaps an output (only an addend that is its own output, stride = rows, may)");
+                return 0;
+            }
+        }
+    }
+    HIP_TRY(hipSetDevice(tensors[0]->device));
+    hipStream_t s = (hipStream_t)stream;
+    Workspace &ws = workspace_for(tensors[0]->device, s);
+    Epilogue epi;
+    epi.add = d_addends;
+    epi.ldadd = addend_strides;
+    return launch_group(const_cast<QmvDeviceTensor *const *>(tensors), count, d_inputs, batch_count, d_outputs, s,
+                        ws, epi);
+}
+
+QMV_API int qmv_device_matvec_swiglu_f32(qmv_device_tensor gate, qmv_device_tensor up, const float *d_inputs,
+                                         int batch_count, float *d_outputs, void *stream)
+{
+    if (gate == nullptr || up == nullptr) {
+        set_error("invalid fused SwiGLU arguments");
+        return 0;
+    }
+    if (!group_args_ok(&gate, 1, d_inputs, batch_count, &d_outputs)) return 0;
+    if (up->ggml_type != gate->ggml_type || up->cols != gate->cols || up->rows != gate->rows ||
+        up->device != gate->device) {
+        set_error("gate and up must share type, shape and device");
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(gate->device));
+    hipStream_t s = (hipStream_t)stream;
+    Workspace &ws = workspace_for(gate->device, s);
+    QmvDeviceTensor *const pair[2] = {gate, up};
+    float *const outs[2] = {d_outputs, d_outputs}; /* only job 0's output is written */
+    Epilogue epi;
+    epi.swiglu = true;
+    return launch_group(pair, 2, d_inputs, batch_count, outs, s, ws, epi);
+}
+
 QMV_API int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *d_input, float *d_logits,
                                          int *d_result, void *stream)
 {
@@ -761,7 +897,9 @@ QMV_API int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *
     HIP_TRY(hipSetDevice(tensor->device));
     hipStream_t s = (hipStream_t)stream;
     Workspace &ws = workspace_for(tensor->device, s);
-    return launch_group(&tensor, 1, d_input, 1, &d_logits, s, ws, d_result);
+    Epilogue epi;
+    epi.argmax = d_result;
+    return launch_group(&tensor, 1, d_input, 1, &d_logits, s, ws, epi);
 }
 
 QMV_API int qmv_device_embed_rows_f32(qmv_device_tensor t, const int *d_token_ids, int count, float *d_output,

@@ -4,7 +4,9 @@ ctypes access to the CPU oracle for the MI355X packed matvec path:
   * ``liboracle.so``: the plain-C restatement of the reference's scalar path
     (qmv_oracle.c; header qmv_oracle.h lists what pins each function);
   * ``_ref/libref_scalar.so`` / ``_ref/libref_avx2.so``: the reference's own
-    src/quantization.cpp + src/quantized_matvec.cpp compiled from source by
+    src/quantization.cpp + src/quantized_matvec.cpp (and the decode-step
+    element operations of src/tensor.cpp, src/transformer_ops.cpp) compiled
+    from source by
     ``oracle/Makefile`` (present wherever they were built; they travel with the
     repository tree but are never committed).
 
@@ -60,6 +62,9 @@ _ORACLE_SIGS = {
     "oracle_dequantize_rows": (_i, [_vp, _i, _i, _vp]),
     "oracle_row_stats_f64": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "oracle_greedy_argmax": (_i, [_vp, _i, _vp]),
+    "oracle_add_f32": (_i, [_vp, _vp, _i, _vp]),
+    "oracle_rms_norm_f32": (_i, [_vp, _vp, _i, ctypes.c_float, _vp]),
+    "oracle_swiglu_f32": (_i, [_vp, _vp, _i, _vp]),
 }
 
 _REF_SIGS = {
@@ -76,6 +81,9 @@ _REF_SIGS = {
     "ref_q6_k_unpack_value": (_i, [_vp, _i, _vp, _vp]),
     "ref_quantized_tensor_matvec_f32": (_i, [_vp, _vp, _i, _vp, _i]),
     "ref_quantized_tensor_matmul_f32": (_i, [_vp, _vp, _i, _i, _vp, _i]),
+    "ref_tensor_add_f32": (_i, [_vp, _vp, _i, _vp]),
+    "ref_tensor_rms_norm_f32": (_i, [_vp, _vp, _i, ctypes.c_float, _vp]),
+    "ref_transformer_swiglu_f32": (_i, [_vp, _vp, _i]),
 }
 
 _cache = {}
@@ -182,3 +190,31 @@ def greedy_argmax(logits):
     tok = ctypes.c_int(-7)
     ok = lib().oracle_greedy_argmax(_p(logits), logits.size, ctypes.byref(tok))
     return ok, tok.value
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def add(left, right):
+    """tensor_add_f32 restated: (ok, left + right in fp32)."""
+    left, right = _f32(left), _f32(right)
+    out = np.empty_like(left)
+    ok = lib().oracle_add_f32(_p(left), _p(right), left.size, _p(out))
+    return ok, out
+
+
+def rms_norm(x, weight, epsilon):
+    """tensor_rms_norm_f32 restated on one vector: (ok, output)."""
+    x, weight = _f32(x), _f32(weight)
+    out = np.empty_like(x)
+    ok = lib().oracle_rms_norm_f32(_p(x), _p(weight), x.size, float(epsilon), _p(out))
+    return ok, out
+
+
+def swiglu(gate, up):
+    """transformer_swiglu_f32 restated, out of place: (ok, up * silu(gate))."""
+    gate, up = _f32(gate), _f32(up)
+    out = np.empty_like(gate)
+    ok = lib().oracle_swiglu_f32(_p(gate), _p(up), gate.size, _p(out))
+    return ok, out

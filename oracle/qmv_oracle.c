@@ -403,3 +403,43 @@ int oracle_greedy_argmax(const float *logits, int vocab_size, int *token_id)
     *token_id = best;
     return 1;
 }
+
+/* ---- Decode-step element operations ----------------------------------- */
+
+int oracle_add_f32(const float *left, const float *right, int length, float *output)
+{
+    /* src/tensor.cpp:11-17: null pointers and non-positive lengths fail. */
+    if (!left || !right || !output || length <= 0) return 0;
+    for (int i = 0; i < length; ++i) output[i] = left[i] + right[i];
+    return 1;
+}
+
+int oracle_rms_norm_f32(const float *input, const float *weight, int length, float epsilon,
+                        float *output)
+{
+    /* src/tensor.cpp:116-122: epsilon <= 0 fails (a NaN epsilon does not). */
+    if (!input || !weight || !output || length <= 0 || epsilon <= 0) return 0;
+    /* :124-127: sum of squares in index order, in fp32. */
+    float sum_sq = 0.0f;
+    for (int i = 0; i < length; ++i) {
+        const float sq = input[i] * input[i];
+        sum_sq += sq;
+    }
+    /* :129: sqrt(mean + epsilon); :131-133: (x / denom) * weight. */
+    const float denom = sqrtf(sum_sq / (float)length + epsilon);
+    for (int i = 0; i < length; ++i) output[i] = (input[i] / denom) * weight[i];
+    return 1;
+}
+
+int oracle_swiglu_f32(const float *gate, const float *up, int length, float *output)
+{
+    /* src/transformer_ops.cpp:169-172: null pointers and length <= 0 fail. */
+    if (!gate || !up || !output || length <= 0) return 0;
+    for (int i = 0; i < length; ++i) {
+        /* :163-165 silu(x) = x / (1 + exp(-x)); :175 up * silu(gate). */
+        const float g = gate[i];
+        const float silu = g / (1.0f + expf(-g));
+        output[i] = up[i] * silu;
+    }
+    return 1;
+}

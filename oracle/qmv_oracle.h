@@ -23,6 +23,16 @@
  *                             with the reference's scalar build in oracle/_ref
  *   oracle_greedy_argmax      tie/NaN cases of src/sampler.cpp:29-51 and numpy
  *                             argmax
+ *   oracle_add_f32            reference KAT (tests/tensor_reference_test.cpp:
+ *                             50-58), numpy's fp32 add, the reference build
+ *   oracle_rms_norm_f32       reference KAT (tests/tensor_reference_test.cpp:
+ *                             84-93), a float64 closed form (including inputs
+ *                             small enough that epsilon dominates), the
+ *                             invalid-argument table (:154-156), bit-for-bit
+ *                             equality with the reference's scalar build
+ *   oracle_swiglu_f32         reference KAT (tests/transformer_ops_reference_
+ *                             test.cpp:95-108), a float64 closed form, bit-for-
+ *                             bit equality with the reference's scalar build
  */
 #ifndef QMV_ORACLE_H
 #define QMV_ORACLE_H
@@ -91,6 +101,16 @@ int oracle_row_stats_f64(const OracleView *matrix, const float *input,
 
 /* sampler_greedy_sample: lowest id on ties, 0 and -1 on any non-finite logit. */
 int oracle_greedy_argmax(const float *logits, int vocab_size, int *token_id);
+
+/* Decode-step element operations between the projections. */
+/* tensor_add_f32 (src/tensor.cpp:5-23): output[i] = left[i] + right[i]. */
+int oracle_add_f32(const float *left, const float *right, int length, float *output);
+/* tensor_rms_norm_f32 (src/tensor.cpp:99-136). */
+int oracle_rms_norm_f32(const float *input, const float *weight, int length, float epsilon,
+                        float *output);
+/* transformer_swiglu_f32 (src/transformer_ops.cpp:163-176), out of place:
+ * output[i] = up[i] * silu(gate[i]); output may equal gate. */
+int oracle_swiglu_f32(const float *gate, const float *up, int length, float *output);
 
 #ifdef __cplusplus
 }

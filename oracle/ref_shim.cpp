@@ -8,6 +8,8 @@
  */
 #include "quantization.h"
 #include "quantized_matvec.h"
+#include "tensor.h"
+#include "transformer_ops.h"
 
 #include <string.h>
 
@@ -61,4 +63,21 @@ REF_EXPORT int ref_quantized_tensor_matmul_f32(const GgufQuantizedTensorView *m,
                                                int xn, int batch, float *y, int yn)
 {
     return quantized_tensor_matmul_f32(m, x, xn, batch, y, yn);
+}
+
+/* Decode-step element operations (src/tensor.cpp, src/transformer_ops.cpp). */
+REF_EXPORT int ref_tensor_add_f32(const float *a, const float *b, int n, float *out)
+{
+    return tensor_add_f32(a, b, n, out);
+}
+
+REF_EXPORT int ref_tensor_rms_norm_f32(const float *x, const float *w, int n, float eps, float *out)
+{
+    return tensor_rms_norm_f32(x, w, n, eps, out);
+}
+
+/* In place on gate, as the reference defines it. */
+REF_EXPORT int ref_transformer_swiglu_f32(float *gate, const float *up, int n)
+{
+    return transformer_swiglu_f32(gate, up, n);
 }

@@ -111,8 +111,31 @@ def test_invalid_sampler_and_device_args_fail_without_gpu(qmv):
     assert lib.qmv_device_greedy_argmax_f32(None, 10, None, None) == 0
     assert lib.qmv_device_matvec_argmax_f32(None, None, None, None, None) == 0
     assert lib.qmv_device_embed_rows_f32(None, None, 1, None, None) == 0
+    assert lib.qmv_device_matvec_add_group_f32(None, 1, None, 1, None, None, None, None) == 0
+    assert lib.qmv_device_matvec_swiglu_f32(None, None, None, 1, None, None) == 0
     assert lib.qmv_device_tensor_create(None, None) == 0
     assert lib.qmv_dequantize_rows_f32(None, 0, 1, x.ctypes.data) == 0
+
+
+def test_rms_norm_argument_table_without_gpu(qmv):
+    """src/tensor.cpp:116-122 (null pointers, length <= 0, epsilon <= 0), plus
+    batch_count <= 0 and the overlap rule; all rejected before any HIP call
+    (the addresses are compared, never dereferenced)."""
+    lib = qmv.hip_lib()
+    buf = np.zeros(64, dtype=np.float32)
+    a = buf.ctypes.data
+    x, w, y = a, a + 4 * 16, a + 4 * 32
+    assert lib.qmv_device_rms_norm_f32(None, w, 8, 1, 1e-6, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, None, 8, 1, 1e-6, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 1, 1e-6, None, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 0, 1, 1e-6, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 0, 1e-6, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 1, 0.0, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 1, -1.0, y, None) == 0
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 1, 1e-6, x + 4, None) == 0  # part of the input
+    assert lib.qmv_device_rms_norm_f32(x, w, 8, 1, 1e-6, w + 4, None) == 0  # the weight
+    assert "RMSNorm" in qmv.last_error()
+    assert (buf == 0).all()
 
 
 def test_synth_is_deterministic_and_distributed(qmv):

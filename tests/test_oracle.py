@@ -431,3 +431,172 @@ def test_row_helpers_against_independent_forms(oracle, t):
     fin = np.isfinite(prod).all(axis=1)
     assert np.allclose(dot[fin], prod[fin].sum(axis=1), rtol=1e-12, atol=1e-300)
     assert np.allclose(absdot[fin], np.abs(prod[fin]).sum(axis=1), rtol=1e-12, atol=1e-300)
+
+
+# ---- decode-step element operations ----------------------------------------------------
+
+U32 = 2.0 ** -24  # unit roundoff of binary32
+
+
+def _rms_norm_f64(x, w, eps):
+    x64 = x.astype(np.float64)
+    return x64 / np.sqrt(np.mean(x64 * x64) + float(np.float32(eps))) * w.astype(np.float64)
+
+
+def _swiglu_f64(g, u):
+    g64 = g.astype(np.float64)
+    return u.astype(np.float64) * (g64 / (1.0 + np.exp(-g64)))
+
+
+# Relative error allowed against the float64 closed form. RMSNorm: the fp32
+# sum of squares in index order is off by about sqrt(n) * u relative
+# (3.6e-6 at n = 3584; a worst case of n * u / 2 = 1.1e-4 needs adversarial
+# data), halved by the square root, plus three roundings; 2e-5 leaves a 5x
+# margin and still rejects the plausible mistakes below (a dropped epsilon,
+# n - 1 for n, a missing square root, a shifted weight index).
+RMS_REL = 2e-5
+SWIGLU_ULPS = 4
+
+
+def _rms_inputs(n, scale, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(n) * scale).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    return x, w
+
+
+def _rms_close(y, x, w, eps):
+    ref = _rms_norm_f64(x, w, eps)
+    return bool(np.all(np.abs(y.astype(np.float64) - ref) <= RMS_REL * np.abs(ref) + 1e-30))
+
+
+def test_element_op_kats(oracle):
+    """tests/tensor_reference_test.cpp:50-58, 84-93 and
+    tests/transformer_ops_reference_test.cpp:95-103, at the reference's 1e-5."""
+    ok, y = oracle.add([0.75, 0.85, 1.0], [0.0, -3.5, 5.0])
+    assert ok == 1 and np.all(np.abs(y - np.array([0.75, -2.65, 6.0], np.float32)) <= 1e-5)
+    ok, y = oracle.rms_norm([1.0, 1.0], [2.0, 3.0], 3.0)
+    assert ok == 1 and y.tolist() == [1.0, 1.5]  # exact: sqrt(1 + 3) = 2
+    ok, y = oracle.swiglu([0.0, 1.0, -1.0], [4.0, 2.0, 5.0])
+    assert ok == 1 and np.all(np.abs(y - np.array([0.0, 1.462117, -1.344707], np.float32)) <= 1e-5)
+
+
+def test_element_op_invalid_arguments(oracle):
+    """src/tensor.cpp:11-17, 116-122 and src/transformer_ops.cpp:169-172; the
+    reference's own table is tests/tensor_reference_test.cpp:145-156."""
+    lib = oracle.lib()
+    v = np.ones(3, dtype=np.float32)
+    o = np.zeros(3, dtype=np.float32)
+    assert lib.oracle_add_f32(None, _p(v), 3, _p(o)) == 0
+    assert lib.oracle_add_f32(_p(v), _p(v), 0, _p(o)) == 0
+    assert lib.oracle_rms_norm_f32(None, _p(v), 3, 1e-5, _p(o)) == 0
+    assert lib.oracle_rms_norm_f32(_p(v), None, 3, 1e-5, _p(o)) == 0
+    assert lib.oracle_rms_norm_f32(_p(v), _p(v), 3, 0.0, _p(o)) == 0
+    assert lib.oracle_rms_norm_f32(_p(v), _p(v), 3, -1.0, _p(o)) == 0
+    assert lib.oracle_rms_norm_f32(_p(v), _p(v), -3, 1e-5, _p(o)) == 0
+    assert lib.oracle_swiglu_f32(None, _p(v), 3, _p(o)) == 0
+    assert lib.oracle_swiglu_f32(_p(v), _p(v), 0, _p(o)) == 0
+    # epsilon <= 0 is the only epsilon check: NaN passes it, as in the reference.
+    assert lib.oracle_rms_norm_f32(_p(v), _p(v), 3, float("nan"), _p(o)) == 1
+
+
+def test_add_is_fp32_add(oracle):
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(5000).astype(np.float32)
+    b = (rng.standard_normal(5000) * 1e3).astype(np.float32)
+    ok, y = oracle.add(a, b)
+    assert ok == 1 and np.array_equal(y.view(np.uint32), (a + b).view(np.uint32))
+
+
+@pytest.mark.parametrize("n,scale", [(3584, 1.0), (3584, 1e-3), (896, 30.0), (1536, 1e-4), (7, 1.0)])
+def test_rms_norm_against_float64(oracle, n, scale):
+    """The 1e-3 and 1e-4 scales put the mean square at or below epsilon, so a
+    dropped or misplaced epsilon fails."""
+    x, w = _rms_inputs(n, scale, n)
+    ok, y = oracle.rms_norm(x, w, 1e-6)
+    assert ok == 1 and _rms_close(y, x, w, 1e-6)
+
+
+def test_rms_norm_constant_input(oracle):
+    """x = c everywhere: y = c / sqrt(c^2 + eps) * w exactly up to three roundings."""
+    x = np.full(1000, 0.5, np.float32)
+    w = np.full(1000, 3.0, np.float32)
+    ok, y = oracle.rms_norm(x, w, 0.75)  # mean 0.25 + 0.75 = 1: y = 0.5 * 3 exactly
+    assert ok == 1 and np.all(y == 1.5)
+
+
+def _rms_mistakes():
+    def no_eps(x, w, eps):
+        x64 = x.astype(np.float64)
+        return (x64 / np.sqrt(np.mean(x64 * x64)) * w).astype(np.float32)
+
+    def n_minus_one(x, w, eps):
+        x64 = x.astype(np.float64)
+        return (x64 / np.sqrt(np.sum(x64 * x64) / (x.size - 1) + eps) * w).astype(np.float32)
+
+    def no_sqrt(x, w, eps):
+        x64 = x.astype(np.float64)
+        return (x64 / (np.mean(x64 * x64) + eps) * w).astype(np.float32)
+
+    def shifted_weight(x, w, eps):
+        return _rms_norm_f64(x, np.roll(w, 1), eps).astype(np.float32)
+
+    return [no_eps, n_minus_one, no_sqrt, shifted_weight]
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_rms_norm_check_rejects_planted_mistakes(case):
+    """Each plausible RMSNorm mistake fails the float64 check on at least one
+    of the inputs test_rms_norm_against_float64 uses."""
+    wrong = _rms_mistakes()[case]
+    caught = False
+    for n, scale in [(3584, 1.0), (3584, 1e-3), (896, 30.0), (1536, 1e-4)]:
+        x, w = _rms_inputs(n, scale, n)
+        caught |= not _rms_close(wrong(x, w, 1e-6), x, w, 1e-6)
+    assert caught
+
+
+def test_swiglu_against_float64(oracle):
+    rng = np.random.default_rng(5)
+    g = np.concatenate([rng.standard_normal(20000) * 4, [0.0, -0.0, 90.0, -90.0, 1e-30, -1e-30]]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    ok, y = oracle.swiglu(g, u)
+    ref = _swiglu_f64(g, u)
+    assert ok == 1
+    # The absolute floor covers gates near -90, where exp(-g) overflows fp32
+    # and silu is -0 instead of about -1e-37.
+    assert np.all(np.abs(y - ref) <= SWIGLU_ULPS * U32 * 2 * np.abs(ref) + 1e-30)
+    # Large negative gates: exp overflows to inf and silu is -0 times up.
+    ok, y = oracle.swiglu(np.array([-200.0], np.float32), np.array([2.0], np.float32))
+    assert ok == 1 and y[0] == 0.0
+
+
+def test_element_ops_bit_identical_to_reference_scalar_build(oracle):
+    ref = _ref_or_skip(oracle, "scalar")
+    rng = np.random.default_rng(21)
+    for n, scale in [(3584, 1.0), (3584, 1e-3), (18944, 2.0), (5, 1.0)]:
+        x, w = _rms_inputs(n, scale, n + 1)
+        y_ref = np.empty_like(x)
+        assert ref.ref_tensor_rms_norm_f32(_p(x), _p(w), n, 1e-6, _p(y_ref)) == 1
+        ok, y = oracle.rms_norm(x, w, 1e-6)
+        assert ok == 1 and np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+        g = (rng.standard_normal(n) * 3).astype(np.float32)
+        u = rng.standard_normal(n).astype(np.float32)
+        gate = g.copy()
+        assert ref.ref_transformer_swiglu_f32(_p(gate), _p(u), n) == 1
+        ok, y = oracle.swiglu(g, u)
+        assert ok == 1 and np.array_equal(y.view(np.uint32), gate.view(np.uint32))
+        s_ref = np.empty_like(x)
+        assert ref.ref_tensor_add_f32(_p(x), _p(w), n, _p(s_ref)) == 1
+        assert np.array_equal(oracle.add(x, w)[1].view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_reference_avx2_element_ops_within_tolerance(oracle):
+    """The as-deployed build contracts the sum of squares into FMAs, so its
+    RMSNorm differs in the last bits; it meets the same float64 bound."""
+    ref = _ref_or_skip(oracle, "avx2")
+    for n, scale in [(3584, 1.0), (3584, 1e-3), (896, 30.0)]:
+        x, w = _rms_inputs(n, scale, n)
+        y = np.empty_like(x)
+        assert ref.ref_tensor_rms_norm_f32(_p(x), _p(w), n, 1e-6, _p(y)) == 1
+        assert _rms_close(y, x, w, 1e-6)
