@@ -16,8 +16,10 @@ resident weights), the HBM traffic per
 launch from the committed rocprofv3 counter summary when it covers this
 kernel and workload, and the CPU baseline (the reference's own x86 build,
 AVX2 + OpenMP, on a bounded sample). `extra` adds the same set at M=8, the
-per-step p10/p50/p90, eager (ungraphed) launch time and a measured streaming
-read bandwidth.
+per-step p10/p50/p90, eager (ungraphed) launch time, a measured streaming
+read bandwidth, the vocabulary projection with greedy sampling, and the same
+layers as a device-resident decode step with its element operations
+(biases, residuals, RMSNorm, SwiGLU).
 """
 import argparse
 import ctypes
@@ -228,6 +230,69 @@ def vocab_bench(qmv, hip, stream, reps):
     return out
 
 
+def graph_us(hip, stream, fns, reps):
+    """Capture fns (each enqueues on `stream`) once; µs per replay between two
+    HIP events on the stream."""
+    for fn in fns:
+        fn()
+    stream.synchronize()
+    g = hip.Graph(stream)
+    g.begin()
+    for fn in fns:
+        fn()
+    g.end()
+    g.replay()
+    stream.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_ms(e1) / reps * 1e3
+
+
+def decode_ops_bench(qmv, hip, stream, layers, reps):
+    """The same 28 layers as a device-resident decode step: the projections
+    with the element operations between them on device buffers (RMSNorm ->
+    q/k/v + bias -> o + residual -> RMSNorm -> gate/up SwiGLU -> down +
+    residual; RoPE and attention are not on this path, so o reads the query
+    rows). 6 launches per layer, captured once and replayed between two HIP
+    events; then each kind of launch alone (its 28 or 56 launches of a step
+    in one graph) for the time per launch."""
+    D = hip.DeviceBuffer
+    rng = np.random.default_rng(90)
+    vec = lambda n, s: D.from_array((s * rng.standard_normal(n)).astype(np.float32))
+    x = D.from_array(qmv.synth_normal(HIDDEN, seed=91))
+    w_attn, w_ffn = D.from_array(np.ones(HIDDEN, np.float32)), D.from_array(np.ones(HIDDEN, np.float32))
+    bq, bk, bv = vec(HIDDEN, 0.1), vec(KV, 0.1), vec(KV, 0.1)
+    h, q, k, v, act = D(4 * HIDDEN), D(4 * HIDDEN), D(4 * KV), D(4 * KV), D(4 * INTER)
+    sp = stream.handle
+    eps = 1e-6
+    ops = []  # (kind, fn) in step order
+    for T in layers:
+        ops += [
+            ("rms_norm", lambda: qmv.device_rms_norm(x.ptr, w_attn.ptr, HIDDEN, 1, eps, h.ptr, sp)),
+            ("qkv_bias", lambda T=T: qmv.device_matvec_add_group(
+                [T["q"], T["k"], T["v"]], h.ptr, 1, [bq.ptr, bk.ptr, bv.ptr], [0, 0, 0], [q.ptr, k.ptr, v.ptr], sp)),
+            ("o_residual", lambda T=T: qmv.device_matvec_add_group([T["o"]], q.ptr, 1, [x.ptr], [HIDDEN], [x.ptr],
+                                                                   sp)),
+            ("rms_norm", lambda: qmv.device_rms_norm(x.ptr, w_ffn.ptr, HIDDEN, 1, eps, h.ptr, sp)),
+            ("gate_up_swiglu", lambda T=T: qmv.device_matvec_swiglu(T["gate"], T["up"], h.ptr, 1, act.ptr, sp)),
+            ("down_residual", lambda T=T: qmv.device_matvec_add_group([T["down"]], act.ptr, 1, [x.ptr], [HIDDEN],
+                                                                      [x.ptr], sp)),
+        ]
+    out = {"ms_per_step": round(graph_us(hip, stream, [fn for _, fn in ops], reps) / 1e3, 4),
+           "launches_per_step": len(ops)}
+    out["residual_finite"] = bool(np.isfinite(x.to_array(np.float32, (HIDDEN,))).all())
+    per = {}
+    for kind in dict.fromkeys(k for k, _ in ops):
+        fns = [fn for k, fn in ops if k == kind]
+        per[kind] = round(graph_us(hip, stream, fns, reps) / len(fns), 2)
+    out["us_per_launch"] = per
+    return out
+
+
 def committed_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
     summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by a copy-kernel
@@ -327,6 +392,11 @@ def main():
                                "weight_gbs": round(total_bytes / (r8["elapsed"] / max(5, args.steps // 5)) / 1e9, 1),
                                "positions_per_s": round(8 / (r8["ms_per_step"] * 1e-3), 1)}
         extra["vocab_projection"] = vocab_bench(qmv, hip, stream, max(10, args.steps // 2))
+        if M == 1:
+            ops = decode_ops_bench(qmv, hip, stream, layers, max(10, args.steps // 2))
+            ops["projection_set_ms"] = round(main_run["ms_per_step"], 4)
+            ops["element_ops_overhead_ms"] = round(ops["ms_per_step"] - main_run["ms_per_step"], 4)
+            extra["decode_step_with_element_ops"] = ops
         probe = importlib.import_module("my-inference-engine_amd.probe")
         extra["hbm_read_probe"] = probe.read_bandwidth(1 << 30, 512, 10)
         extra["hbm_fraction_of_read_probe"] = round(value / extra["hbm_read_probe"]["gbs"], 4)

@@ -1419,29 +1419,76 @@ argmax_stage2(const float *__restrict__ bval, const int *__restrict__ bidx, cons
 }
 
 /* RMSNorm (tensor_rms_norm_f32, src/tensor.cpp:99-136) of one vector per
- * workgroup: out = (x / sqrt(mean(x^2) + eps)) * w. The sum of squares runs
- * in a fixed order (each thread strides the vector, then a butterfly within
- * the wave and the four wave sums in order), so results are deterministic;
- * the division and square root are IEEE-rounded. Every thread reads the
- * elements it writes after the workgroup barrier, so out may be x itself. */
-#define QMV_NORM_THREADS 256
+ * workgroup: out = (x / sqrt(mean(x^2) + eps)) * w. A decode-step vector
+ * (3584 floats) is one 16-byte load per thread, held in registers from the
+ * sum of squares to the output, so the kernel costs one load round, one
+ * reduction and one store round. The sum of squares runs in a fixed order
+ * (each thread's elements in index order, a butterfly within the wave, then
+ * the wave sums in wave order), so results are deterministic; the division
+ * and square root are IEEE-rounded. Each element is read and written by
+ * one thread only (the one whose stride covers it), so out may be x itself. */
+#define QMV_NORM_THREADS 1024
+#define QMV_NORM_REGS 2 /* 16-byte words per thread kept in registers */
 __global__ void __launch_bounds__(QMV_NORM_THREADS)
 rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, float *out)
 {
     const float *xv = x + (size_t)blockIdx.x * n;
     float *ov = out + (size_t)blockIdx.x * n;
+    const int tid = threadIdx.x;
+    /* 16-byte path when every row start is 16-byte aligned. */
+    const bool vec = (n & 3) == 0 && (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+    const int n4 = vec ? n >> 2 : 0;
+    float4 r[QMV_NORM_REGS];
     float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += QMV_NORM_THREADS) s += xv[i] * xv[i];
+#pragma unroll
+    for (int j = 0; j < QMV_NORM_REGS; ++j) {
+        const int i = tid + j * QMV_NORM_THREADS;
+        r[j] = i < n4 ? reinterpret_cast<const float4 *>(xv)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < QMV_NORM_REGS; ++j) {
+        s += r[j].x * r[j].x;
+        s += r[j].y * r[j].y;
+        s += r[j].z * r[j].z;
+        s += r[j].w * r[j].w;
+    }
+    for (int i = tid + QMV_NORM_REGS * QMV_NORM_THREADS; i < n4; i += QMV_NORM_THREADS) {
+        const float4 v = reinterpret_cast<const float4 *>(xv)[i];
+        s += v.x * v.x;
+        s += v.y * v.y;
+        s += v.z * v.z;
+        s += v.w * v.w;
+    }
+    if (!vec)
+        for (int i = tid; i < n; i += QMV_NORM_THREADS) s += xv[i] * xv[i];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
     __shared__ float wave_sum[QMV_NORM_THREADS / 64];
-    if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = s;
+    if ((tid & 63) == 0) wave_sum[tid >> 6] = s;
     __syncthreads();
     float total = wave_sum[0];
 #pragma unroll
     for (int v = 1; v < QMV_NORM_THREADS / 64; ++v) total += wave_sum[v];
     const float denom = sqrtf(total / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += QMV_NORM_THREADS) ov[i] = (xv[i] / denom) * w[i];
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < QMV_NORM_REGS; ++j) {
+            const int i = tid + j * QMV_NORM_THREADS;
+            if (i < n4) {
+                const float4 g = reinterpret_cast<const float4 *>(w)[i];
+                reinterpret_cast<float4 *>(ov)[i] = make_float4((r[j].x / denom) * g.x, (r[j].y / denom) * g.y,
+                                                                (r[j].z / denom) * g.z, (r[j].w / denom) * g.w);
+            }
+        }
+        for (int i = tid + QMV_NORM_REGS * QMV_NORM_THREADS; i < n4; i += QMV_NORM_THREADS) {
+            const float4 v = reinterpret_cast<const float4 *>(xv)[i];
+            const float4 g = reinterpret_cast<const float4 *>(w)[i];
+            reinterpret_cast<float4 *>(ov)[i] =
+                make_float4((v.x / denom) * g.x, (v.y / denom) * g.y, (v.z / denom) * g.z, (v.w / denom) * g.w);
+        }
+    } else {
+        for (int i = tid; i < n; i += QMV_NORM_THREADS) ov[i] = (xv[i] / denom) * w[i];
+    }
 }
 
 /* ---- host-side launchers -------------------------------------------------- */
