@@ -15,7 +15,8 @@ between two HIP events on the stream the kernels run on, over the same
 resident weights), the HBM traffic per
 launch from the committed rocprofv3 counter summary when it covers this
 kernel and workload, and the CPU baseline (the reference's own x86 build,
-AVX2 + OpenMP, on a bounded sample). `extra` adds the same set at M=8, the
+AVX2 + OpenMP, on a bounded sample). `extra` adds the same set at M=8 and at
+M=32 (a prefill chunk of 32 positions per pass over the weights), the
 per-step p10/p50/p90, eager (ungraphed) launch time, a measured streaming
 read bandwidth, the vocabulary projection with greedy sampling, and the same
 layers as a device-resident decode step with its element operations
@@ -82,6 +83,13 @@ def cpu_baseline(qmv, host_layer, batch, seconds):
                       f"OMP_NUM_THREADS={threads})"}
 
 
+def kernel_name(fmt, M):
+    """The kernel a Q4_K / Q6_K launch of M positions runs (default tuning)."""
+    if M >= (7 if fmt == "Q4_K" else 8):
+        return "matvec_mfma_kernel<%s,%d>" % (fmt, M if M <= 8 else 16 if M <= 16 else 32)
+    return "matvec_kernel<%s,%d>" % (fmt, M)
+
+
 def build_launches(lib, layers, acts, outs, M):
     """One step = 4 launches per layer, arguments prepared once."""
     grp_fn = lib.qmv_device_matvec_group_f32
@@ -104,7 +112,7 @@ def build_launches(lib, layers, acts, outs, M):
             w = sum(T[n].packed_bytes for n in names)
             return w + 4 * M * cols + 4 * M * sum(T[n].rows for n in names)
 
-        kq, k6 = "matvec_kernel<Q4_K,%d>" % M, "matvec_kernel<Q6_K,%d>" % M
+        kq, k6 = kernel_name("Q4_K", M), kernel_name("Q6_K", M)
         launches.append((kq, algo(["q", "k", "v"], HIDDEN), grp(["q", "k", "v"], A["attn"])))
         launches.append((kq, algo(["o"], HIDDEN), one("o", A["o"])))
         launches.append((kq, algo(["gate", "up"], HIDDEN), grp(["gate", "up"], A["ffn"])))
@@ -313,7 +321,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=1, help="positions per matvec (1 = decode, <= 8)")
+    ap.add_argument("--batch", type=int, default=1, help="positions per matvec (1 = decode, <= 32)")
     ap.add_argument("--profile-passes", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-graph", action="store_true")
@@ -324,8 +332,8 @@ def main():
         print(f"bench.py measures one GPU only (this path has no multi-GPU mode); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
-    if not 1 <= args.batch <= 8:
-        print("--batch must be in 1..8", file=sys.stderr)
+    if not 1 <= args.batch <= 32:
+        print("--batch must be in 1..32", file=sys.stderr)
         sys.exit(2)
 
     qmv = importlib.import_module("my-inference-engine_amd")
@@ -336,7 +344,7 @@ def main():
     hip.check(hip.rt().hipSetDevice(0), "hipSetDevice")
     stream = hip.Stream()
     M = args.batch
-    MX = max(M, 8)
+    MX = 32  # activation rows per layer: the M = 32 prefill leg reads all of them
 
     # ---- weights: generated per layer on the host, uploaded, host copy dropped
     t0 = time.time()
@@ -385,12 +393,15 @@ def main():
              "kernel_sum_ms_per_step": round(sum(v[1] for v in per_kernel.values()) / passes, 4),
              "kernels": kernels, "upload_s": round(upload_s, 2)}
     if not args.no_extra:
-        if M != 8:
-            l8 = build_launches(lib, layers, acts, outs, 8)
-            r8 = run_set(qmv, hip, stream, l8, max(5, args.steps // 5), 2, not args.no_graph)
-            extra["m8_set"] = {"ms_per_step": round(r8["ms_per_step"], 4),
-                               "weight_gbs": round(total_bytes / (r8["elapsed"] / max(5, args.steps // 5)) / 1e9, 1),
-                               "positions_per_s": round(8 / (r8["ms_per_step"] * 1e-3), 1)}
+        for mb in (8, 32):
+            if mb == M:
+                continue
+            lb = build_launches(lib, layers, acts, outs, mb)
+            rb = run_set(qmv, hip, stream, lb, max(5, args.steps // 5), 2, not args.no_graph)
+            extra[f"m{mb}_set"] = {"ms_per_step": round(rb["ms_per_step"], 4),
+                                   "weight_gbs": round(total_bytes / (rb["elapsed"] / max(5, args.steps // 5)) / 1e9,
+                                                       1),
+                                   "positions_per_s": round(mb / (rb["ms_per_step"] * 1e-3), 1)}
         extra["vocab_projection"] = vocab_bench(qmv, hip, stream, max(10, args.steps // 2))
         if M == 1:
             ops = decode_ops_bench(qmv, hip, stream, layers, max(10, args.steps // 2))

@@ -62,14 +62,15 @@ int qmv_tensor_matvec_f32(const QmvTensorView *matrix, const float *input,
 /*
  * outputs[B,N] = inputs[B,K] * W^T for token-major batches. Replaces
  * quantized_tensor_matmul_f32 (src/quantized_matvec.h:43-50,
- * src/quantized_matvec.cpp:164-224). batch_count must be positive; the
- * device kernels process up to QMV_MAX_BATCH positions per pass.
+ * src/quantized_matvec.cpp:164-224). batch_count must be positive; each
+ * pass over the weights serves up to QMV_MAX_BATCH positions (Q4_K and Q6_K
+ * on the matrix cores) or 8 (Q8_0, Q5_0).
  */
 int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs,
                           int input_count, int batch_count, float *outputs,
                           int output_count);
 
-#define QMV_MAX_BATCH 8
+#define QMV_MAX_BATCH 32
 
 /*
  * Upload a packed tensor now (at model load) instead of on first use, so
@@ -125,6 +126,9 @@ int qmv_device_tensor_info(qmv_device_tensor tensor, int *rows, int *columns,
 /*
  * d_outputs[B,N] = d_inputs[B,K] * W^T with device pointers, enqueued on
  * stream without host synchronisation (1 <= batch_count <= QMV_MAX_BATCH).
+ * Q4_K and Q6_K batches of 9 to 32 positions (prefill chunks larger than the
+ * reference's 8, src/qwen2_internal.h:7) read the weights once, on the
+ * matrix cores; Q8_0 and Q5_0 batches run in launches of 8.
  */
 int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_inputs,
                           int batch_count, float *d_outputs, void *stream);
@@ -239,7 +243,8 @@ int qmv_device_count(void);
  * target_waves, if set, instead grows the units per wave until about that
  * many waves cover the launch. Q4_K and Q6_K batches of at least
  * mfma_min_batch positions (default 7 for Q4_K, 8 for Q6_K; a value above
- * QMV_MAX_BATCH turns it off) run on the matrix cores. Defaults may also come from the
+ * QMV_MAX_BATCH turns it off, and then batches run in launches of 8 on the
+ * VALU path) run on the matrix cores. Defaults may also come from the
  * QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP /
  * QMV_MFMA_MIN_BATCH environment variables. Any setting stays within the row
  * tolerance: the plan only changes the summation order, and a given plan

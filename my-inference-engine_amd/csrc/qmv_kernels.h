@@ -11,6 +11,10 @@
 
 #define QMV_MAX_WAVES 8
 #define QMV_MAX_JOBS 8
+/* Positions per launch: the VALU kernels take up to 8, the matrix-core
+ * kernels (Q4_K, Q6_K) up to 32 in blocks of 16. */
+#define QMV_VALU_MAX_POSITIONS 8
+#define QMV_MFMA_MAX_POSITIONS 32
 
 namespace qmv {
 
@@ -41,6 +45,7 @@ struct MatvecParams {
     float *partials;
     unsigned *counters; /* all zero between launches */
     int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
+    int positions;    /* positions in this launch: M, or 9..M for the M = 16, 32 prefill kernels */
     /* Fused greedy argmax (single tensor, M = 1; result non-null): tile and
      * group candidates (argmax_words(tiles) words), group and top arrival
      * counts (argmax_counts(tiles), zero between launches) and the result. */

@@ -849,7 +849,7 @@ __device__ __forceinline__ float swiglu_value(float g, float u)
  * up * silu(gate) to job 0's output, then resets the count. */
 template <int M>
 __device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork &w, int lane, int row, bool valid,
-                                            const float (&v)[M])
+                                            int npos, const float (&v)[M])
 {
     const MatvecJob &out = p.job[0];
     float *mine = p.pair_vals + ((size_t)w.job * out.tiles + w.tile) * M * 64 + lane;
@@ -867,7 +867,7 @@ __device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork 
         const float o = load_partial(other + m * 64);
         const float g = w.job == 0 ? v[m] : o;
         const float u = w.job == 0 ? o : v[m];
-        if (valid) out.y[(size_t)m * out.ldy + row] = swiglu_value(g, u);
+        if (valid && m < npos) out.y[(size_t)m * out.ldy + row] = swiglu_value(g, u);
     }
     if (lane == 0) __hip_atomic_store(p.pair_count + w.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -878,22 +878,24 @@ __device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork 
  * lane, so an addend that is the output itself (a residual added in place)
  * is safe. */
 template <int M>
-__device__ __forceinline__ void emit_tile(const MatvecParams &p, const WgWork &w, int lane, float (&v)[M])
+__device__ __forceinline__ void emit_tile(const MatvecParams &p, const WgWork &w, int lane, int npos, float (&v)[M])
 {
     const MatvecJob &job = p.job[w.job];
     const int row = w.tile * 64 + lane;
     const bool valid = row < job.rows;
     if (job.add != nullptr && valid) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) v[m] += job.add[(size_t)m * job.ldadd + row];
+        for (int m = 0; m < M; ++m)
+            if (m < npos) v[m] += job.add[(size_t)m * job.ldadd + row];
     }
     if (p.swiglu) {
-        swiglu_pair<M>(p, w, lane, row, valid, v);
+        swiglu_pair<M>(p, w, lane, row, valid, npos, v);
         return;
     }
     if (valid) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) job.y[(size_t)m * job.ldy + row] = v[m];
+        for (int m = 0; m < M; ++m)
+            if (m < npos) job.y[(size_t)m * job.ldy + row] = v[m];
     }
     if constexpr (M == 1)
         if (p.argmax_result) tile_argmax(p, w.tile, valid, row, v[0], lane);
@@ -911,7 +913,7 @@ __device__ __forceinline__ void emit_tile(const MatvecParams &p, const WgWork &w
  * clearing between launches. */
 template <int M>
 __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork &w, int nwaves, int lane,
-                                            const float (*red)[M][64])
+                                            const float (*red)[M][64], int npos = M)
 {
     const MatvecJob &job = p.job[w.job];
     float sum[M];
@@ -923,7 +925,7 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
     }
 
     if (job.splits == 1) {
-        emit_tile<M>(p, w, lane, sum);
+        emit_tile<M>(p, w, lane, npos, sum);
         return;
     }
 
@@ -941,7 +943,7 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
 #pragma unroll
     for (int m = 0; m < M; ++m) fin[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
     if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    emit_tile<M>(p, w, lane, fin);
+    emit_tile<M>(p, w, lane, npos, fin);
 }
 
 /* kOne: every wave takes at most one unit (units_per_wave == 1), so no
@@ -1046,14 +1048,21 @@ __device__ __forceinline__ void x_limbs(const float (&xv)[KL], bool valid, V &h,
     }
 }
 
-template <int M>
-__device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
-                                              f32x4_t (&acc)[4])
+template <int P>
+__device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int npos,
+                                              f32x4_t (&acc)[P][4])
 {
     const int kc = lane >> 4, n = lane & 15;
-    const bool valid = n < M;
-    /* Lanes past the batch read position 0 (in bounds) and use zeros. */
-    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
+    /* Position block pb covers positions 16 pb .. 16 pb + 15; this lane
+     * supplies position 16 pb + n. Lanes past the batch read position 0 (in
+     * bounds) and use zeros. */
+    bool valid[P];
+    const float *xp[P];
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb) {
+        valid[pb] = 16 * pb + n < npos;
+        xp[pb] = xu + (size_t)(valid[pb] ? 16 * pb + n : 0) * ldx + 8 * kc;
+    }
     /* This lane's bytes of row 16g + n: header, and the 8 qs bytes of its
      * k-chunk in 64-weight group c (plane 1 + 2c + kc/2). */
     const uint8_t *rowp = slab + n * 16;
@@ -1066,67 +1075,82 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     for (int g = 0; g < 4; ++g) q[0][g] = *(const uint2 *)(qsp + g * 256);
     const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
                            (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
-    float xv[2][8];
-    load_x<8>(xv[0], xp);
+    float xv[2][P][8];
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb) load_x<8>(xv[0][pb], xp[pb]);
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         const int c = sb >> 1;
         const bool high = sb & 1;
         /* Next sub-block's activations, and at a group's start the next
          * group's codes, load while this sub-block runs. */
-        if (sb + 1 < 8) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
+        if (sb + 1 < 8)
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb)
+                load_x<8>(xv[(sb + 1) & 1][pb], ptr_after(xp[pb] + 32 * (sb + 1), acc[0][0][0]));
         if (!high && c + 1 < 4) {
-            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[1][0]);
+            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[0][1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
         }
-        bf16x8_t a0, a1, a2;
-        x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
         /* High nibbles are used in place as 16 * q; 1/16 is folded into the
-         * sub-block scale (exact). */
+         * sub-block scale (exact). The codes are decoded once and serve
+         * every position block. */
         const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
         bf16x8_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const uint32_t lo = codes(after(q[c & 1][g].x, acc[g][0]) & mask);
-            const uint32_t hi = codes(after(q[c & 1][g].y, acc[g][0]) & mask);
+            const uint32_t lo = codes(after(q[c & 1][g].x, acc[0][g][0]) & mask);
+            const uint32_t hi = codes(after(q[c & 1][g].y, acc[0][g][0]) & mask);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 b[g][j] = (__bf16)ubyte(lo, j);
                 b[g][4 + j] = (__bf16)ubyte(hi, j);
             }
         }
-        f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
+        float sa[4], sm[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, xs, 0, 0, 0);
+        for (int pb = 0; pb < P; ++pb) {
+            bf16x8_t a0, a1, a2;
+            x_limbs<8>(xv[sb & 1][pb], valid[pb], a0, a1, a2);
+            f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, xs, 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, ones, xs, 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, ones, xs, 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            /* Decoded here, not hoisted: the scales of one sub-block live. */
-            const float dep = d[g][0];
-            const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep), after(h[g].w, dep)};
-            const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
-            uint32_t scw, mw;
-            if (sb < 4) {
-                scw = hg.y & 0x3f3f3f3fu;
-                mw = hg.z & 0x3f3f3f3fu;
-            } else {
-                scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
-                mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
+            if (pb == 0) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    /* Decoded here, not hoisted: the scales of one sub-block live. */
+                    const float dep = d[g][0];
+                    const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep),
+                                      after(h[g].w, dep)};
+                    const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
+                    uint32_t scw, mw;
+                    if (sb < 4) {
+                        scw = hg.y & 0x3f3f3f3fu;
+                        mw = hg.z & 0x3f3f3f3fu;
+                    } else {
+                        scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
+                        mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
+                    }
+                    sa[g] = dd * ubyte(scw, sb & 3);
+                    if (high) sa[g] *= 0.0625f;
+                    sm[g] = dmin * ubyte(mw, sb & 3);
+                }
             }
-            float sa = dd * ubyte(scw, sb & 3);
-            if (high) sa *= 0.0625f;
-            const float sm = dmin * ubyte(mw, sb & 3);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[g][j] = fmaf(sa, d[g][j], fmaf(-sm, xs[j], acc[g][j]));
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[pb][g][j] = fmaf(sa[g], d[g][j], fmaf(-sm[g], xs[j], acc[pb][g][j]));
         }
     }
 }
@@ -1135,13 +1159,18 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
  * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
  * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
  * ql/qh words serves four of them. */
-template <int M>
-__device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
-                                              f32x4_t (&acc)[4])
+template <int P>
+__device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int npos,
+                                              f32x4_t (&acc)[P][4])
 {
     const int kc = lane >> 4, n = lane & 15;
-    const bool valid = n < M;
-    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 4 * kc;
+    bool valid[P];
+    const float *xp[P];
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb) {
+        valid[pb] = 16 * pb + n < npos;
+        xp[pb] = xu + (size_t)(valid[pb] ? 16 * pb + n : 0) * ldx + 4 * kc;
+    }
     const uint8_t *wp = slab + n * 16 + 4 * kc; /* this lane's dword of row 16g + n in a plane */
     uint4 sc[4];
     float dg[4];
@@ -1158,8 +1187,9 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         w[0][g][1] = *(const uint32_t *)(wp + 2 * 1024 + g * 256);
         w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
     }
-    float xv[2][4];
-    load_x<4>(xv[0], xp);
+    float xv[2][P][4];
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb) load_x<4>(xv[0][pb], xp[pb]);
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
         const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
@@ -1167,11 +1197,13 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         const int j = 8 * G + 2 * r + hf;
         if (t + 1 < 16) {
             const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
-            load_x<4>(xv[(t + 1) & 1], ptr_after(xp + 16 * jn, acc[0][0]));
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb)
+                load_x<4>(xv[(t + 1) & 1][pb], ptr_after(xp[pb] + 16 * jn, acc[0][0][0]));
         }
         if (r == 0 && pr + 1 < 4) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
-            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[1][0]);
+            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[0][1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 w[(pr + 1) & 1][g][0] = *(const uint32_t *)(np + (4 * Gn + hn) * 1024 + g * 256);
@@ -1179,71 +1211,88 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
                 w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
             }
         }
-        bf16x4_t a0, a1, a2;
-        x_limbs<4>(xv[t & 1], valid, a0, a1, a2);
         bf16x4_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[g][0]);
-            const uint32_t hw = after(w[pr & 1][g][2], acc[g][0]);
+            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[0][g][0]);
+            const uint32_t hw = after(w[pr & 1][g][2], acc[0][g][0]);
             const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
 #pragma unroll
             for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
         }
-        f32x4_t d[4];
+        float s[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int pb = 0; pb < P; ++pb) {
+            bf16x4_t a0, a1, a2;
+            x_limbs<4>(xv[t & 1][pb], valid[pb], a0, a1, a2);
+            f32x4_t d[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float s = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
+            if (pb == 0)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(s, d[g][i], acc[g][i]);
+                for (int g = 0; g < 4; ++g) s[g] = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(s[g], d[g][i], acc[pb][g][i]);
         }
     }
 }
 
 /* Same launch plan, combine and split-K protocol as matvec_kernel; each wave
- * runs its units on the matrix cores and scatters its 64 rows x M positions
- * into the combine buffer. */
-/* Four resident waves per SIMD (at most 128 VGPRs): these waves are short
- * and latency-bound, so residency matters more than registers. */
+ * runs its units on the matrix cores and scatters its 64 rows x positions
+ * into the combine buffer. M <= 8 is one position block with exactly M
+ * positions; M = 16 or 32 (prefill batches) is one or two blocks of 16 that
+ * share each decoded code tile, with the launch's positions (p.positions,
+ * at most M) in the first rows. */
+/* Four resident waves per SIMD (at most 128 VGPRs) for one position block:
+ * these waves are short and latency-bound, so residency matters more than
+ * registers; two blocks keep twice the accumulators. */
 template <int FMT, int M>
-__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) __attribute__((amdgpu_waves_per_eu(M <= 16 ? 4 : 2)))
 matvec_mfma_kernel(MatvecParams p)
 {
     constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    constexpr int P = (M + 15) / 16;
     __shared__ float red[QMV_MAX_WAVES][M][64];
 
+    const int npos = M <= 8 ? M : p.positions;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WgWork w = locate(p, wave);
     const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
 
-    f32x4_t acc[4];
+    f32x4_t acc[P][4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     for (int u = w.u_begin; u < w.u_end; ++u) {
         if constexpr (FMT == QMV_FMT_Q4_K)
-            q4k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+            q4k_unit_mfma<P>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, npos, acc);
         else
-            q6k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+            q6k_unit_mfma<P>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, npos, acc);
     }
 
     const int kc = lane >> 4, n = lane & 15;
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int pb = 0; pb < P; ++pb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (4 * kc + j < M) red[wave][4 * kc + j][16 * g + n] = acc[g][j];
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = 16 * pb + 4 * kc + j;
+                if (pos < M) red[wave][pos][16 * g + n] = pos < npos ? acc[pb][g][j] : 0.0f;
+            }
     __syncthreads();
     if (wave != 0) return;
-    finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
+    finish_tile<M>(p, w, blockDim.x >> 6, lane, red, npos);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------
@@ -1502,11 +1551,15 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
             return hipGetLastError();
         }
     }
+    if constexpr (M > 8) {
+        return hipErrorInvalidValue; /* prefill batches exist on the matrix cores only */
+    } else {
     if (p.units_per_wave == 1)
         hipLaunchKernelGGL((matvec_kernel<FMT, M, true>), dim3(grid), dim3(waves * 64), 0, s, p);
     else
         hipLaunchKernelGGL((matvec_kernel<FMT, M, false>), dim3(grid), dim3(waves * 64), 0, s, p);
     return hipGetLastError();
+    }
 }
 
 #define QMV_FOR_M(MACRO, FMT)                                                                          \
@@ -1522,13 +1575,27 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
     default: break;                                                                                    \
     }
 
+/* Prefill batches of 9..32 positions: Q4_K and Q6_K on the matrix cores. */
+#define QMV_FOR_M_WIDE(MACRO, FMT)                                                                     \
+    switch (m) {                                                                                       \
+    case 16: return MACRO(FMT, 16);                                                                    \
+    case 32: return MACRO(FMT, 32);                                                                    \
+    default: break;                                                                                    \
+    }
+
 #define QMV_LAUNCH(FMT, M) launch_matvec_fm<FMT, M>(p, grid, waves, s)
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
 {
     switch (fmt) {
-    case QMV_FMT_Q4_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K) break;
-    case QMV_FMT_Q6_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K) break;
+    case QMV_FMT_Q4_K:
+        QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K)
+        QMV_FOR_M_WIDE(QMV_LAUNCH, QMV_FMT_Q4_K)
+        break;
+    case QMV_FMT_Q6_K:
+        QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K)
+        QMV_FOR_M_WIDE(QMV_LAUNCH, QMV_FMT_Q6_K)
+        break;
     case QMV_FMT_Q8_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q8_0) break;
     case QMV_FMT_Q5_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q5_0) break;
     default: break;

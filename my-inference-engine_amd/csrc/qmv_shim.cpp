@@ -410,7 +410,7 @@ std::atomic<int> g_target_waves{env_int("QMV_TARGET_WAVES", 0)};
 std::atomic<int> g_force_u{env_int("QMV_UNITS_PER_WAVE", 0)};
 std::atomic<int> g_force_w{env_int("QMV_WAVES_PER_GROUP", 0)};
 /* Smallest batch run on the matrix cores (Q4_K, Q6_K); above QMV_MAX_BATCH
- * turns them off. By default the batch from which they beat the VALU path on
+ * turns them off (batches then run in launches of 8 on the VALU path). By default the batch from which they beat the VALU path on
  * MI355X at Qwen2.5-7B layer shapes: 7 for Q4_K, 8 for Q6_K (its code
  * assembly costs more VALU per weight on the matrix-core path). */
 std::atomic<int> g_mfma_min_batch{env_int("QMV_MFMA_MIN_BATCH", 0)};
@@ -470,29 +470,40 @@ struct Epilogue {
     bool swiglu = false;               /* tensors (gate, up): out[0] = up * silu(gate) */
 };
 
-/* Enqueue one launch over `count` tensors sharing the input. */
-int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
-                 hipStream_t stream, Workspace &ws, const Epilogue &epi = Epilogue())
+/* Enqueue one launch over `count` tensors sharing the input, for positions
+ * [b0, b0 + batch) of the caller's batch (the caller's pointers are offset
+ * here). */
+int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, int batch,
+                 float *const *d_out, hipStream_t stream, Workspace &ws, const Epilogue &epi)
 {
     const QmvDeviceTensor *t0 = ts[0];
     long long total_tiles = 0;
     for (int i = 0; i < count; ++i) total_tiles += ts[i]->tiles;
     const Plan plan = plan_for(total_tiles, t0->units);
+    const bool mfma = use_matrix_cores(t0->geo.format, batch);
+    /* Kernel instance: exactly `batch` positions, or a 16 / 32 position
+     * matrix-core kernel with the batch in its first rows. */
+    const int mt = batch <= QMV_VALU_MAX_POSITIONS ? batch : batch <= 16 ? 16 : 32;
+    if (mt > QMV_VALU_MAX_POSITIONS && !mfma) {
+        set_error("more than 8 positions per launch need the matrix-core path");
+        return 0;
+    }
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
     p.njobs = count;
-    p.x = d_in;
+    p.x = d_in + (size_t)b0 * t0->cols;
     p.ldx = t0->cols;
     p.cols = t0->cols;
     p.units = t0->units;
     p.units_per_wave = plan.units_per_wave;
+    p.positions = batch;
     size_t partials = 0, counters = 0;
     long long wg = 0;
     for (int i = 0; i < count; ++i) {
         qmv::MatvecJob &j = p.job[i];
         j.w = ts[i]->data;
-        j.y = d_out[i];
+        j.y = d_out[i] + (size_t)b0 * ts[i]->rows;
         j.rows = ts[i]->rows;
         j.ldy = ts[i]->rows;
         j.tiles = ts[i]->tiles;
@@ -502,11 +513,11 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         j.partial_offset = (int)partials;
         j.counter_offset = (int)counters;
         if (epi.add && epi.add[i]) {
-            j.add = epi.add[i];
+            j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
             j.ldadd = epi.ldadd[i];
         }
         if (plan.splits > 1) {
-            partials += (size_t)ts[i]->tiles * plan.splits * batch * 64;
+            partials += (size_t)ts[i]->tiles * plan.splits * mt * 64;
             counters += (size_t)ts[i]->tiles;
         }
         wg += (long long)ts[i]->tiles * plan.splits;
@@ -519,7 +530,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
             set_error("fused SwiGLU takes two tensors (gate, up) with equal rows");
             return 0;
         }
-        partials += (size_t)2 * t0->tiles * batch * 64;
+        partials += (size_t)2 * t0->tiles * mt * 64;
         counters += (size_t)t0->tiles;
         p.swiglu = 1;
     }
@@ -527,7 +538,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         set_error("launch too large");
         return 0;
     }
-    p.matrix_cores = use_matrix_cores(t0->geo.format, batch);
+    p.matrix_cores = mfma;
     std::lock_guard<std::mutex> lock(ws.mu);
     if (!workspace_reserve(ws, stream, partials, counters)) return 0;
     p.partials = ws.partials;
@@ -537,7 +548,7 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         p.pair_count = ws.counters + pair_count;
     }
     if (epi.argmax) {
-        if (count != 1 || batch != 1 || epi.swiglu) {
+        if (count != 1 || batch != 1 || b0 != 0 || epi.swiglu) {
             set_error("fused argmax takes one tensor and one position");
             return 0;
         }
@@ -547,18 +558,27 @@ int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         p.argmax_result = epi.argmax;
         p.argmax_tiles = t0->tiles;
     }
-    HIP_TRY(qmv::launch_matvec(t0->geo.format, p, batch, (int)wg, plan.waves, stream));
+    HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, plan.waves, stream));
     return 1;
 }
 
-/* Batches of more than QMV_MAX_BATCH positions run as consecutive launches. */
-int launch_batched(QmvDeviceTensor *t, const float *d_in, int batch, float *d_out, hipStream_t stream,
-                   Workspace &ws)
+/* Positions per launch for a batch: up to 32 on the matrix cores (Q4_K and
+ * Q6_K prefill), else 8. */
+int chunk_positions(int fmt, int batch)
 {
-    for (int b0 = 0; b0 < batch; b0 += QMV_MAX_BATCH) {
-        const int nb = batch - b0 < QMV_MAX_BATCH ? batch - b0 : QMV_MAX_BATCH;
-        float *out = d_out + (size_t)b0 * t->rows;
-        if (!launch_group(&t, 1, d_in + (size_t)b0 * t->cols, nb, &out, stream, ws)) return 0;
+    const int wide = batch < QMV_MFMA_MAX_POSITIONS ? batch : QMV_MFMA_MAX_POSITIONS;
+    return wide > QMV_VALU_MAX_POSITIONS && use_matrix_cores(fmt, wide) ? QMV_MFMA_MAX_POSITIONS
+                                                                           : QMV_VALU_MAX_POSITIONS;
+}
+
+/* Enqueue a batch of any size as launches of up to chunk_positions(). */
+int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
+                 hipStream_t stream, Workspace &ws, const Epilogue &epi = Epilogue())
+{
+    const int chunk = chunk_positions(ts[0]->geo.format, batch);
+    for (int b0 = 0; b0 < batch; b0 += chunk) {
+        const int nb = batch - b0 < chunk ? batch - b0 : chunk;
+        if (!launch_chunk(ts, count, d_in, b0, nb, d_out, stream, ws, epi)) return 0;
     }
     return 1;
 }
@@ -578,7 +598,8 @@ int host_matmul(const QmvTensorView *m, const float *in, int in_count, int batch
     memcpy(c->h_in, in, nin * sizeof(float));
     HIP_TRY(hipMemcpyAsync(c->d_in, c->h_in, nin * sizeof(float), hipMemcpyHostToDevice, c->stream));
     Workspace &ws = workspace_for(c->device, c->stream);
-    if (!launch_batched(t.get(), c->d_in, batch, c->d_out, c->stream, ws)) return 0;
+    QmvDeviceTensor *tp = t.get();
+    if (!launch_group(&tp, 1, c->d_in, batch, &c->d_out, c->stream, ws)) return 0;
     HIP_TRY(hipMemcpyAsync(c->h_out, c->d_out, nout * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     int armed = g_fail_next.load();

@@ -262,7 +262,7 @@ def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
 # kernel variant) and runs Q4_K batches of 7 or more and Q6_K batches of 8 on
 # the matrix cores; the others run the two-unit pipelined variant, one wave per
 # workgroup, whole-K workgroups (no split), target-sized units, the VALU path
-# for every batch (mfma_min_batch 9) and the matrix cores from batch 2.
+# for every batch of up to 8 (mfma_min_batch 9) and the matrix cores from batch 2.
 PLANS = [(0, 0, 0, 0), (0, 2, 0, 0), (0, 3, 7, 0), (0, 1, 1, 0), (0, 1, 8, 0), (2048, 0, 0, 0), (0, 2, 1, 0),
          (0, 8, 8, 0), (0, 5, 3, 0), (0, 0, 0, 9), (0, 2, 0, 9), (0, 3, 7, 9), (0, 0, 0, 2), (0, 2, 0, 2)]
 

@@ -1,0 +1,169 @@
+"""GPU parity of prefill batches of more than 8 positions (the reference
+prefills in chunks of QWEN2_PREFILL_CHUNK_SIZE = 8, src/qwen2_internal.h:7,
+through quantized_tensor_matmul_f32, src/quantized_matvec.cpp:164-224).
+Q4_K and Q6_K batches of 9..32 positions run as one launch on the matrix
+cores (position blocks of 16 sharing each decoded code tile); larger batches
+and the other formats run as consecutive launches.
+
+Bars: every row of every position within 1e-5 * sum |w x| of the oracle;
+and, because a position's arithmetic on the matrix cores does not depend on
+the other positions of its launch, a wide launch is bit-identical to the
+same positions run in launches of at most 8 on the matrix cores.
+"""
+import numpy as np
+import pytest
+
+import _blocks as B
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def hip(qmv):
+    import importlib
+    return importlib.import_module("my-inference-engine_amd.hip_runtime")
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _check(oracle, raw, t, rows, cols, x, y, what):
+    worst = 0.0
+    for b in range(x.shape[0]):
+        y_ref = oracle.matvec(raw, t, rows, cols, x[b])
+        _, absdot = oracle.row_stats(raw, t, rows, cols, x[b])
+        err = np.abs(y[b].astype(np.float64) - y_ref)
+        assert (err <= TOL * absdot).all(), f"{what}: position {b}"
+        worst = max(worst, float(np.max(err / np.maximum(absdot, 1e-300))))
+    log(f"{what}: worst err/sum|wx| {worst:.2e}")
+
+
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q8_0, B.Q5_0])
+@pytest.mark.parametrize("batch", [9, 16, 17, 32, 33, 40])
+def test_prefill_batches_match_oracle(qmv, oracle, gpu, t, batch):
+    rows = 200
+    cols = 5 * B.BLOCK_ELEMENTS[t] if t in (B.Q4_K, B.Q6_K) else 7 * 32 + 512
+    raw = qmv.synth_tensor(t, rows, cols, seed=300 + batch)
+    x = qmv.synth_normal(batch * cols, seed=301 + batch).reshape(batch, cols)
+    v = qmv.make_view(raw, t, rows, cols)
+    y = qmv.matvec(v, x)
+    _check(oracle, raw, t, rows, cols, x, y, f"type {t} {rows}x{cols} B={batch}")
+    qmv.release_tensor(v.data)
+
+
+@pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 18944, 3584), (B.Q6_K, 3584, 18944), (B.Q4_K, 3584, 3584),
+                                         (B.Q4_K, 512, 3584), (B.Q4_K, 8960, 1536)])
+def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
+    batch = 32
+    raw = qmv.synth_tensor(t, rows, cols, seed=310)
+    x = qmv.synth_normal(batch * cols, seed=311).reshape(batch, cols)
+    v = qmv.make_view(raw, t, rows, cols)
+    y = qmv.matvec(v, x)
+    _check(oracle, raw, t, rows, cols, x, y, f"type {t} {rows}x{cols} B=32")
+    qmv.release_tensor(v.data)
+
+
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K])
+@pytest.mark.parametrize("batch,parts", [(32, [8, 8, 8, 8]), (24, [8, 8, 8]), (12, [8, 4]), (20, [8, 8, 4]),
+                                         (9, [5, 4])])
+def test_wide_launch_bit_identical_to_narrow(qmv, gpu, hip, t, batch, parts):
+    """One launch of `batch` positions against the same positions in launches
+    of at most 8, all on the matrix cores (mfma_min_batch 1), on device
+    buffers."""
+    rows, cols = 1000, 3584
+    raw = qmv.synth_tensor(t, rows, cols, seed=320)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+    x = qmv.synth_normal(batch * cols, seed=321)
+    dx = hip.DeviceBuffer.from_array(x)
+    wide = hip.DeviceBuffer(4 * batch * rows)
+    narrow = hip.DeviceBuffer(4 * batch * rows)
+    s = hip.Stream()
+    qmv.set_launch_tuning(0, 0, 0, 1)
+    try:
+        dt.matvec(dx.ptr, batch, wide.ptr, s.handle)
+        b0 = 0
+        for n in parts:
+            dt.matvec(dx.ptr + 4 * b0 * cols, n, narrow.ptr + 4 * b0 * rows, s.handle)
+            b0 += n
+        s.synchronize()
+    finally:
+        qmv.set_launch_tuning(0, 0, 0, 0)
+    assert np.array_equal(_bits(wide.to_array(np.float32, (batch, rows))),
+                          _bits(narrow.to_array(np.float32, (batch, rows))))
+    dt.close()
+
+
+def test_prefill_epilogues(qmv, oracle, gpu, hip):
+    """Bias addend and fused SwiGLU on a 32-position launch (the positions
+    past the batch inside the kernel's position block are never stored)."""
+    t, rows, cols, batch = B.Q4_K, 1000, 3584, 27
+    raw_g = qmv.synth_tensor(t, rows, cols, seed=330)
+    raw_u = qmv.synth_tensor(t, rows, cols, seed=331)
+    dg = qmv.DeviceTensor(qmv.make_view(raw_g, t, rows, cols))
+    du = qmv.DeviceTensor(qmv.make_view(raw_u, t, rows, cols))
+    x = qmv.synth_normal(batch * cols, seed=332).reshape(batch, cols)
+    dx = hip.DeviceBuffer.from_array(x)
+    s = hip.Stream()
+    g, u = hip.DeviceBuffer(4 * (batch + 5) * rows), hip.DeviceBuffer(4 * batch * rows)
+    g.fill(0x7f)  # sentinel rows past the batch must survive
+    qmv.device_matvec_group([dg, du], dx.ptr, batch, [g.ptr, u.ptr], s.handle)
+    s.synchronize()
+    gate = g.to_array(np.float32, (batch + 5, rows))
+    assert np.all(_bits(gate[batch:]) == 0x7f7f7f7f)
+    gate, up = gate[:batch], u.to_array(np.float32, (batch, rows))
+    _check(oracle, raw_g, t, rows, cols, x, gate, "gate B=27")
+    bias = np.random.default_rng(333).standard_normal(rows).astype(np.float32)
+    db = hip.DeviceBuffer.from_array(bias)
+    out = hip.DeviceBuffer(4 * batch * rows)
+    qmv.device_matvec_add_group([dg], dx.ptr, batch, [db.ptr], [0], [out.ptr], s.handle)
+    act = hip.DeviceBuffer(4 * batch * rows)
+    qmv.device_matvec_swiglu(dg, du, dx.ptr, batch, act.ptr, s.handle)
+    s.synchronize()
+    assert np.array_equal(_bits(out.to_array(np.float32, (batch, rows))), _bits(gate + bias[None, :]))
+    got = act.to_array(np.float32, (batch, rows))
+    for b in range(batch):
+        ok, ref = oracle.swiglu(gate[b], up[b])
+        assert ok == 1
+        assert (np.abs(got[b].astype(np.float64) - ref) <= 4 * 2.0 ** -23 * np.abs(ref) + 1e-30).all(), b
+    dg.close()
+    du.close()
+
+
+def test_prefill_graph_replay(qmv, gpu, hip):
+    t, rows, cols, batch = B.Q6_K, 3584, 18944, 32
+    raw = qmv.synth_tensor(t, rows, cols, seed=340)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
+    dx = hip.DeviceBuffer.from_array(qmv.synth_normal(batch * cols, seed=341))
+    dy = hip.DeviceBuffer(4 * batch * rows)
+    s = hip.Stream()
+    dt.matvec(dx.ptr, batch, dy.ptr, s.handle)
+    s.synchronize()
+    eager = dy.to_array(np.float32, (batch * rows,))
+    g = hip.Graph(s)
+    g.begin()
+    dt.matvec(dx.ptr, batch, dy.ptr, s.handle)
+    g.end()
+    for i in range(3):
+        dy.fill(0)
+        g.replay()
+        s.synchronize()
+        assert np.array_equal(_bits(dy.to_array(np.float32, (batch * rows,))), _bits(eager)), i
+        dt.matvec(dx.ptr, batch, dy.ptr, s.handle)
+        s.synchronize()
+    dt.close()
+
+
+def test_device_batch_limit(qmv, gpu, hip):
+    dt = qmv.DeviceTensor(qmv.make_view(qmv.synth_tensor(B.Q4_K, 64, 256, seed=350), B.Q4_K, 64, 256))
+    dx = hip.DeviceBuffer(4 * 33 * 256)
+    dy = hip.DeviceBuffer(4 * 33 * 64)
+    with pytest.raises(qmv.QmvError):
+        dt.matvec(dx.ptr, 33, dy.ptr, 0)
+    dt.close()
