@@ -15,6 +15,8 @@
  * kernels (Q4_K, Q6_K) up to 32 in blocks of 16. */
 #define QMV_VALU_MAX_POSITIONS 8
 #define QMV_MFMA_MAX_POSITIONS 32
+/* Tiles (one per wave) per prefill workgroup. */
+#define QMV_PF_TILES 4
 
 namespace qmv {
 
@@ -45,7 +47,7 @@ struct MatvecParams {
     float *partials;
     unsigned *counters; /* all zero between launches */
     int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
-    int positions;    /* positions in this launch: M, or 9..M for the M = 16, 32 prefill kernels */
+    int positions;    /* positions in this launch (the prefill kernel's position rows past it are padding) */
     /* Fused greedy argmax (single tensor, M = 1; result non-null): tile and
      * group candidates (argmax_words(tiles) words), group and top arrival
      * counts (argmax_counts(tiles), zero between launches) and the result. */
@@ -74,6 +76,9 @@ hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, f
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
                          int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
                          hipStream_t s);
+/* Prefill launch (Q4_K / Q6_K, 9..32 positions): grid = sum over jobs of
+ * ceil(tiles / 4) tile groups x splits. */
+hipError_t launch_prefill(int fmt, const MatvecParams &p, int grid, hipStream_t s);
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out,
                            hipStream_t s);
 hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,

@@ -1048,21 +1048,14 @@ __device__ __forceinline__ void x_limbs(const float (&xv)[KL], bool valid, V &h,
     }
 }
 
-template <int P>
-__device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int npos,
-                                              f32x4_t (&acc)[P][4])
+template <int M>
+__device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
+                                              f32x4_t (&acc)[4])
 {
     const int kc = lane >> 4, n = lane & 15;
-    /* Position block pb covers positions 16 pb .. 16 pb + 15; this lane
-     * supplies position 16 pb + n. Lanes past the batch read position 0 (in
-     * bounds) and use zeros. */
-    bool valid[P];
-    const float *xp[P];
-#pragma unroll
-    for (int pb = 0; pb < P; ++pb) {
-        valid[pb] = 16 * pb + n < npos;
-        xp[pb] = xu + (size_t)(valid[pb] ? 16 * pb + n : 0) * ldx + 8 * kc;
-    }
+    const bool valid = n < M;
+    /* Lanes past the batch read position 0 (in bounds) and use zeros. */
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
     /* This lane's bytes of row 16g + n: header, and the 8 qs bytes of its
      * k-chunk in 64-weight group c (plane 1 + 2c + kc/2). */
     const uint8_t *rowp = slab + n * 16;
@@ -1075,27 +1068,306 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     for (int g = 0; g < 4; ++g) q[0][g] = *(const uint2 *)(qsp + g * 256);
     const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
                            (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
-    float xv[2][P][8];
-#pragma unroll
-    for (int pb = 0; pb < P; ++pb) load_x<8>(xv[0][pb], xp[pb]);
+    float xv[2][8];
+    load_x<8>(xv[0], xp);
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         const int c = sb >> 1;
         const bool high = sb & 1;
         /* Next sub-block's activations, and at a group's start the next
          * group's codes, load while this sub-block runs. */
-        if (sb + 1 < 8)
+        if (sb + 1 < 8) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
+        if (!high && c + 1 < 4) {
+            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[1][0]);
 #pragma unroll
-            for (int pb = 0; pb < P; ++pb)
-                load_x<8>(xv[(sb + 1) & 1][pb], ptr_after(xp[pb] + 32 * (sb + 1), acc[0][0][0]));
+            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
+        }
+        bf16x8_t a0, a1, a2;
+        x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
+        /* High nibbles are used in place as 16 * q; 1/16 is folded into the
+         * sub-block scale (exact). */
+        const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        bf16x8_t b[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lo = codes(after(q[c & 1][g].x, acc[g][0]) & mask);
+            const uint32_t hi = codes(after(q[c & 1][g].y, acc[g][0]) & mask);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                b[g][j] = (__bf16)ubyte(lo, j);
+                b[g][4 + j] = (__bf16)ubyte(hi, j);
+            }
+        }
+        f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            /* Decoded here, not hoisted: the scales of one sub-block live. */
+            const float dep = d[g][0];
+            const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep), after(h[g].w, dep)};
+            const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
+            uint32_t scw, mw;
+            if (sb < 4) {
+                scw = hg.y & 0x3f3f3f3fu;
+                mw = hg.z & 0x3f3f3f3fu;
+            } else {
+                scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
+                mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
+            }
+            float sa = dd * ubyte(scw, sb & 3);
+            if (high) sa *= 0.0625f;
+            const float sm = dmin * ubyte(mw, sb & 3);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[g][j] = fmaf(sa, d[g][j], fmaf(-sm, xs[j], acc[g][j]));
+        }
+    }
+}
+
+/* Q6_K sub-block j = 8G + 2r + hf (16 weights) takes its low nibbles from
+ * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
+ * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
+ * ql/qh words serves four of them. */
+template <int M>
+__device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
+                                              f32x4_t (&acc)[4])
+{
+    const int kc = lane >> 4, n = lane & 15;
+    const bool valid = n < M;
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 4 * kc;
+    const uint8_t *wp = slab + n * 16 + 4 * kc; /* this lane's dword of row 16g + n in a plane */
+    uint4 sc[4];
+    float dg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        sc[g] = ld16(slab + 12 * 1024 + (16 * g + n) * 16);
+        dg[g] = f16_bits_to_f32(*(const unsigned short *)(slab + 13312 + (16 * g + n) * 2));
+    }
+    /* Words of pair (G, hf) and the next pair: ql for r & 1 = 0, 1 and qh. */
+    uint32_t w[2][4][3];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        w[0][g][0] = *(const uint32_t *)(wp + 0 * 1024 + g * 256);
+        w[0][g][1] = *(const uint32_t *)(wp + 2 * 1024 + g * 256);
+        w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
+    }
+    float xv[2][4];
+    load_x<4>(xv[0], xp);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
+        const int G = pr >> 1, hf = pr & 1;
+        const int j = 8 * G + 2 * r + hf;
+        if (t + 1 < 16) {
+            const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
+            load_x<4>(xv[(t + 1) & 1], ptr_after(xp + 16 * jn, acc[0][0]));
+        }
+        if (r == 0 && pr + 1 < 4) {
+            const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
+            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                w[(pr + 1) & 1][g][0] = *(const uint32_t *)(np + (4 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][1] = *(const uint32_t *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
+            }
+        }
+        bf16x4_t a0, a1, a2;
+        x_limbs<4>(xv[t & 1], valid, a0, a1, a2);
+        bf16x4_t b[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[g][0]);
+            const uint32_t hw = after(w[pr & 1][g][2], acc[g][0]);
+            const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
+        }
+        f32x4_t d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float s = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(s, d[g][i], acc[g][i]);
+        }
+    }
+}
+
+/* Same launch plan, combine and split-K protocol as matvec_kernel; each wave
+ * runs its units on the matrix cores and scatters its 64 rows x M positions
+ * into the combine buffer. */
+/* Four resident waves per SIMD (at most 128 VGPRs): these waves are short
+ * and latency-bound, so residency matters more than registers. */
+template <int FMT, int M>
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4)))
+matvec_mfma_kernel(MatvecParams p)
+{
+    constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    __shared__ float red[QMV_MAX_WAVES][M][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WgWork w = locate(p, wave);
+    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
+
+    f32x4_t acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = w.u_begin; u < w.u_end; ++u) {
+        if constexpr (FMT == QMV_FMT_Q4_K)
+            q4k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+        else
+            q6k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+    }
+
+    const int kc = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * kc + j < M) red[wave][4 * kc + j][16 * g + n] = acc[g][j];
+    __syncthreads();
+    if (wave != 0) return;
+    finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
+}
+
+/* ---- Prefill batches (9..32 positions), Q4_K / Q6_K: GEMM-shaped -----------
+ * A workgroup of four waves owns four consecutive 64-row tiles of one tensor
+ * (one per wave) and a range of K-units. For each unit the 256 threads stage
+ * the unit's activations of all positions once, as the three bf16 limbs (see
+ * the matrix-core section above) laid out in MFMA A-fragment order, and each
+ * wave then runs its tile's unit with A read from LDS: an activation is
+ * loaded and split once per workgroup instead of once per wave, and the
+ * codes a wave decodes serve both position blocks of 16. The next unit's
+ * activations are loaded into registers, and its weight headers and first
+ * codes issued, while the current unit computes. Each wave finishes its own
+ * tile with the split-K protocol of finish_tile, so a position's arithmetic
+ * does not depend on the other positions of the launch. */
+#define QMV_PF_WAVES QMV_PF_TILES
+/* Sub-block (Q4_K, of 8) and step (Q6_K, of 16) at which a wave issues the
+ * next unit's first weight loads. */
+#ifndef QMV_PF_NEXT_SB
+#define QMV_PF_NEXT_SB 6
+#endif
+#ifndef QMV_PF_NEXT_T
+#define QMV_PF_NEXT_T 13
+#endif
+#define QMV_PF_POS 32
+
+/* The staging buffer is addressed through an explicit LDS pointer type so
+ * that every access compiles to ds_read / ds_write. */
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+/* An LDS offset that cannot be used before `dep` exists (see ptr_after):
+ * keeps a sub-block's A-fragment reads from being hoisted across the unit. */
+__device__ __forceinline__ int lds_off_after(int off, float dep)
+{
+    asm("" : "+v"(off) : "v"(dep));
+    return off;
+}
+
+/* LDS image of one unit: fragment (limb L, position block pb, k-block b) is
+ * 64 lanes x KL bf16, lane 16 kc + n holding A[n][KL kc .. KL kc + KL - 1] =
+ * limb L of x[16 pb + n][4 KL b + KL kc ..]. */
+template <int KL> struct PfLayout {
+    static constexpr int kBlocks = 256 / (4 * KL);     /* 8 (Q4_K) or 16 (Q6_K) */
+    static constexpr int kFrag = 64 * 2 * KL;          /* bytes per fragment */
+    static constexpr int kChunks = 2 * kBlocks * 64;   /* (pb, b, lane) chunks of KL activations */
+    static constexpr int kPerThread = kChunks / (QMV_PF_WAVES * 64);
+    static constexpr int kBytes = 3 * 2 * kBlocks * kFrag; /* 48 KB */
+    __device__ static int offset(int limb, int pb, int b) { return ((limb * 2 + pb) * kBlocks + b) * kFrag; }
+};
+
+/* Chunk c of a unit: lane = c % 64, block b, position block pb. */
+template <int KL>
+__device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, int tid, float (&xr)[PfLayout<KL>::kPerThread][KL])
+{
+    using L = PfLayout<KL>;
+#pragma unroll
+    for (int i = 0; i < L::kPerThread; ++i) {
+        const int c = tid + i * QMV_PF_WAVES * 64;
+        const int lane = c & 63, rest = c >> 6, b = rest % L::kBlocks, pb = rest / L::kBlocks;
+        const int kc = lane >> 4, n = lane & 15, pos = 16 * pb + n;
+        /* Rows past the batch read position 0 (in bounds) and stage zeros. */
+        const float *src = xu + (size_t)(pos < npos ? pos : 0) * ldx + 4 * KL * b + KL * kc;
+        float v[KL];
+#pragma unroll
+        for (int j = 0; j < KL; ++j) v[j] = src[j];
+#pragma unroll
+        for (int j = 0; j < KL; ++j) xr[i][j] = pos < npos ? v[j] : 0.0f;
+    }
+}
+
+template <int KL>
+__device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid, const float (&xr)[PfLayout<KL>::kPerThread][KL])
+{
+    using L = PfLayout<KL>;
+    typedef __bf16 frag_t __attribute__((__vector_size__(KL * sizeof(__bf16))));
+#pragma unroll
+    for (int i = 0; i < L::kPerThread; ++i) {
+        const int c = tid + i * QMV_PF_WAVES * 64;
+        const int lane = c & 63, rest = c >> 6, b = rest % L::kBlocks, pb = rest / L::kBlocks;
+        frag_t h, m, l;
+        x_limbs<KL>(xr[i], true, h, m, l);
+        typedef __attribute__((address_space(3))) frag_t lds_frag;
+        *(lds_frag *)(lds + L::offset(0, pb, b) + lane * 2 * KL) = h;
+        *(lds_frag *)(lds + L::offset(1, pb, b) + lane * 2 * KL) = m;
+        *(lds_frag *)(lds + L::offset(2, pb, b) + lane * 2 * KL) = l;
+    }
+}
+
+/* One Q4_K unit of this wave's tile against the staged activations; h and q0
+ * hold the unit's headers and group-0 codes on entry and those of `next` on
+ * return (the caller passes the unit itself when there is no next one: the
+ * loads are then harmless repeats, and no branch splits the unrolled body). */
+__device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
+                                            f32x4_t (&acc)[2][4], uint4 (&h)[4], uint2 (&q0)[4])
+{
+    using L = PfLayout<8>;
+    const int kc = lane >> 4, n = lane & 15;
+    const int qoff = (1 + (kc >> 1)) * 1024 + n * 16 + 8 * (kc & 1);
+    const uint8_t *qsp = slab + qoff;
+    uint2 q[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[0][g] = q0[g];
+    uint4 hn[4];
+    uint2 qn[4];
+    const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
+                           (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+        const int c = sb >> 1;
+        const bool high = sb & 1;
         if (!high && c + 1 < 4) {
             const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[0][1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
         }
-        /* High nibbles are used in place as 16 * q; 1/16 is folded into the
-         * sub-block scale (exact). The codes are decoded once and serve
-         * every position block. */
+        if (sb == QMV_PF_NEXT_SB) {
+            const uint8_t *np = (const uint8_t *)ptr_after((const float *)next, acc[0][2][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                hn[g] = ld16(np + n * 16 + g * 256);
+                qn[g] = *(const uint2 *)(np + qoff + g * 256);
+            }
+        }
         const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
         bf16x8_t b[4];
 #pragma unroll
@@ -1110,9 +1382,12 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
         }
         float sa[4], sm[4];
 #pragma unroll
-        for (int pb = 0; pb < P; ++pb) {
-            bf16x8_t a0, a1, a2;
-            x_limbs<8>(xv[sb & 1][pb], valid[pb], a0, a1, a2);
+        for (int pb = 0; pb < 2; ++pb) {
+            typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
+            const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
+            const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, sb));
+            const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, sb));
+            const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, sb));
             f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1128,7 +1403,6 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
             if (pb == 0) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    /* Decoded here, not hoisted: the scales of one sub-block live. */
                     const float dep = d[g][0];
                     const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep),
                                       after(h[g].w, dep)};
@@ -1153,54 +1427,38 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
                     acc[pb][g][j] = fmaf(sa[g], d[g][j], fmaf(-sm[g], xs[j], acc[pb][g][j]));
         }
     }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        h[g] = hn[g];
+        q0[g] = qn[g];
+    }
 }
 
-/* Q6_K sub-block j = 8G + 2r + hf (16 weights) takes its low nibbles from
- * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
- * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
- * ql/qh words serves four of them. */
-template <int P>
-__device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int npos,
-                                              f32x4_t (&acc)[P][4])
+/* Q6_K: sc, dg and w0 (the first (G, hf) pair's words) hold this unit's on
+ * entry and those of `next` on return (as for Q4_K). */
+__device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
+                                            f32x4_t (&acc)[2][4], uint4 (&sc)[4], uint32_t (&dgw)[4],
+                                            uint32_t (&w0)[4][3])
 {
+    using L = PfLayout<4>;
     const int kc = lane >> 4, n = lane & 15;
-    bool valid[P];
-    const float *xp[P];
-#pragma unroll
-    for (int pb = 0; pb < P; ++pb) {
-        valid[pb] = 16 * pb + n < npos;
-        xp[pb] = xu + (size_t)(valid[pb] ? 16 * pb + n : 0) * ldx + 4 * kc;
-    }
-    const uint8_t *wp = slab + n * 16 + 4 * kc; /* this lane's dword of row 16g + n in a plane */
-    uint4 sc[4];
+    const int woff = n * 16 + 4 * kc;
+    const uint8_t *wp = slab + woff;
     float dg[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        sc[g] = ld16(slab + 12 * 1024 + (16 * g + n) * 16);
-        dg[g] = f16_bits_to_f32(*(const unsigned short *)(slab + 13312 + (16 * g + n) * 2));
-    }
-    /* Words of pair (G, hf) and the next pair: ql for r & 1 = 0, 1 and qh. */
+    for (int g = 0; g < 4; ++g) dg[g] = f16_bits_to_f32(dgw[g] & 0xffffu);
     uint32_t w[2][4][3];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        w[0][g][0] = *(const uint32_t *)(wp + 0 * 1024 + g * 256);
-        w[0][g][1] = *(const uint32_t *)(wp + 2 * 1024 + g * 256);
-        w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
-    }
-    float xv[2][P][4];
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-    for (int pb = 0; pb < P; ++pb) load_x<4>(xv[0][pb], xp[pb]);
+        for (int e = 0; e < 3; ++e) w[0][g][e] = w0[g][e];
+    uint4 scn[4];
+    uint32_t dgn[4], wn[4][3];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
-        const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
-        const int G = pr >> 1, hf = pr & 1;
-        const int j = 8 * G + 2 * r + hf;
-        if (t + 1 < 16) {
-            const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
-#pragma unroll
-            for (int pb = 0; pb < P; ++pb)
-                load_x<4>(xv[(t + 1) & 1][pb], ptr_after(xp[pb] + 16 * jn, acc[0][0][0]));
-        }
+        const int pr = t >> 2, r = t & 3;
+        const int G = pr >> 1;
+        const int j = 8 * G + 2 * r + (pr & 1);
         if (r == 0 && pr + 1 < 4) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
             const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[0][1][0]);
@@ -1211,6 +1469,17 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
                 w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
             }
         }
+        if (t == QMV_PF_NEXT_T) {
+            const uint8_t *np = (const uint8_t *)ptr_after((const float *)next, acc[0][2][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                scn[g] = ld16(np + 12 * 1024 + (16 * g + n) * 16);
+                dgn[g] = *(const unsigned short *)(np + 13312 + (16 * g + n) * 2);
+                wn[g][0] = *(const uint32_t *)(np + woff + 0 * 1024 + g * 256);
+                wn[g][1] = *(const uint32_t *)(np + woff + 2 * 1024 + g * 256);
+                wn[g][2] = *(const uint32_t *)(np + woff + 8 * 1024 + g * 256);
+            }
+        }
         bf16x4_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -1218,13 +1487,16 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
             const uint32_t hw = after(w[pr & 1][g][2], acc[0][g][0]);
             const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
+            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f);
         }
         float s[4];
 #pragma unroll
-        for (int pb = 0; pb < P; ++pb) {
-            bf16x4_t a0, a1, a2;
-            x_limbs<4>(xv[t & 1][pb], valid[pb], a0, a1, a2);
+        for (int pb = 0; pb < 2; ++pb) {
+            typedef __attribute__((address_space(3))) const bf16x4_t lds_a;
+            const lds_u8 *la = lds + lds_off_after(lane * 8, acc[pb][3][3]);
+            const bf16x4_t a0 = *(lds_a *)(la + L::offset(0, pb, j));
+            const bf16x4_t a1 = *(lds_a *)(la + L::offset(1, pb, j));
+            const bf16x4_t a2 = *(lds_a *)(la + L::offset(2, pb, j));
             f32x4_t d[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1243,56 +1515,113 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
                 for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(s[g], d[g][i], acc[pb][g][i]);
         }
     }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        sc[g] = scn[g];
+        dgw[g] = dgn[g];
+#pragma unroll
+        for (int e = 0; e < 3; ++e) w0[g][e] = wn[g][e];
+    }
 }
 
-/* Same launch plan, combine and split-K protocol as matvec_kernel; each wave
- * runs its units on the matrix cores and scatters its 64 rows x positions
- * into the combine buffer. M <= 8 is one position block with exactly M
- * positions; M = 16 or 32 (prefill batches) is one or two blocks of 16 that
- * share each decoded code tile, with the launch's positions (p.positions,
- * at most M) in the first rows. */
-/* Four resident waves per SIMD (at most 128 VGPRs) for one position block:
- * these waves are short and latency-bound, so residency matters more than
- * registers; two blocks keep twice the accumulators. */
-template <int FMT, int M>
-__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) __attribute__((amdgpu_waves_per_eu(M <= 16 ? 4 : 2)))
-matvec_mfma_kernel(MatvecParams p)
+/* The workgroup's place in a prefill launch: job, tile group, K-split; this
+ * wave's tile is 4 * group + wave (it may lie past the job's last tile, and
+ * then the wave only helps stage). */
+__device__ __forceinline__ WgWork locate_pf(const MatvecParams &p, int wave)
 {
+    WgWork w;
+    int j = 0;
+    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const MatvecJob &job = p.job[j];
+    const int local = blockIdx.x - job.wg_begin;
+    const int group = local / job.splits;
+    w.job = j;
+    w.split = local - group * job.splits;
+    w.tile = group * QMV_PF_WAVES + wave;
+    w.u_begin = w.split * job.units_per_split;
+    w.u_end = min(w.u_begin + job.units_per_split, p.units);
+    return w;
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams p)
+{
+    constexpr int KL = FMT == QMV_FMT_Q4_K ? 8 : 4;
     constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
-    constexpr int P = (M + 15) / 16;
-    __shared__ float red[QMV_MAX_WAVES][M][64];
+    using L = PfLayout<KL>;
+    static_assert(QMV_PF_WAVES * QMV_PF_POS * 64 * 4 <= L::kBytes, "combine buffer reuses the staging buffer");
+    __shared__ __attribute__((aligned(16))) uint8_t lds_buf[L::kBytes];
+    lds_u8 *lds = (lds_u8 *)lds_buf;
 
-    const int npos = M <= 8 ? M : p.positions;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgWork w = locate(p, wave);
-    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const WgWork w = locate_pf(p, wave);
+    const MatvecJob &job = p.job[w.job];
+    const bool active = w.tile < job.tiles;
+    const int npos = p.positions;
+    const uint8_t *wtile = job.w + (size_t)(active ? w.tile : 0) * p.units * SLAB;
+    const int kc = lane >> 4, n = lane & 15;
 
-    f32x4_t acc[P][4];
+    f32x4_t acc[2][4];
 #pragma unroll
-    for (int pb = 0; pb < P; ++pb)
+    for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) acc[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    /* First unit's weights (this wave's tile) and activations. */
+    uint4 h[4];
+    uint2 q0[4];
+    uint32_t dgw[4], w0[4][3];
+    const uint8_t *first = wtile + (size_t)w.u_begin * SLAB;
+    if constexpr (FMT == QMV_FMT_Q4_K) {
+        const int qoff = (1 + (kc >> 1)) * 1024 + n * 16 + 8 * (kc & 1);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            h[g] = ld16(first + n * 16 + g * 256);
+            q0[g] = *(const uint2 *)(first + qoff + g * 256);
+        }
+    } else {
+        const int woff = n * 16 + 4 * kc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            h[g] = ld16(first + 12 * 1024 + (16 * g + n) * 16);
+            dgw[g] = *(const unsigned short *)(first + 13312 + (16 * g + n) * 2);
+            w0[g][0] = *(const uint32_t *)(first + woff + 0 * 1024 + g * 256);
+            w0[g][1] = *(const uint32_t *)(first + woff + 2 * 1024 + g * 256);
+            w0[g][2] = *(const uint32_t *)(first + woff + 8 * 1024 + g * 256);
+        }
+    }
+    float xr[L::kPerThread][KL];
+    pf_load_x<KL>(p.x + (size_t)w.u_begin * 256, p.ldx, npos, tid, xr);
+
     for (int u = w.u_begin; u < w.u_end; ++u) {
-        if constexpr (FMT == QMV_FMT_Q4_K)
-            q4k_unit_mfma<P>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, npos, acc);
-        else
-            q6k_unit_mfma<P>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, npos, acc);
+        __syncthreads(); /* every wave is done with the previous unit's image */
+        pf_store_limbs<KL>(lds, tid, xr);
+        __syncthreads();
+        if (u + 1 < w.u_end) pf_load_x<KL>(p.x + (size_t)(u + 1) * 256, p.ldx, npos, tid, xr);
+        const uint8_t *slab = wtile + (size_t)u * SLAB;
+        const uint8_t *next = u + 1 < w.u_end ? slab + SLAB : slab;
+        if (active) {
+            if constexpr (FMT == QMV_FMT_Q4_K)
+                q4k_unit_pf(slab, next, lds, lane, acc, h, q0);
+            else
+                q6k_unit_pf(slab, next, lds, lane, acc, h, dgw, w0);
+        }
     }
 
-    const int kc = lane >> 4, n = lane & 15;
+    /* Each wave transposes its tile through its own slice of the (now free)
+     * staging buffer, then finishes the tile on its own. */
+    __syncthreads();
+    float(*red)[QMV_PF_POS][64] = reinterpret_cast<float(*)[QMV_PF_POS][64]>(lds_buf) + wave;
 #pragma unroll
-    for (int pb = 0; pb < P; ++pb)
+    for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int pos = 16 * pb + 4 * kc + j;
-                if (pos < M) red[wave][pos][16 * g + n] = pos < npos ? acc[pb][g][j] : 0.0f;
-            }
-    __syncthreads();
-    if (wave != 0) return;
-    finish_tile<M>(p, w, blockDim.x >> 6, lane, red, npos);
+            for (int j = 0; j < 4; ++j) red[0][16 * pb + 4 * kc + j][16 * g + n] = acc[pb][g][j];
+    if (!active) return;
+    finish_tile<QMV_PF_POS>(p, w, 1, lane, red, npos);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------
@@ -1551,15 +1880,11 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
             return hipGetLastError();
         }
     }
-    if constexpr (M > 8) {
-        return hipErrorInvalidValue; /* prefill batches exist on the matrix cores only */
-    } else {
     if (p.units_per_wave == 1)
         hipLaunchKernelGGL((matvec_kernel<FMT, M, true>), dim3(grid), dim3(waves * 64), 0, s, p);
     else
         hipLaunchKernelGGL((matvec_kernel<FMT, M, false>), dim3(grid), dim3(waves * 64), 0, s, p);
     return hipGetLastError();
-    }
 }
 
 #define QMV_FOR_M(MACRO, FMT)                                                                          \
@@ -1575,27 +1900,13 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
     default: break;                                                                                    \
     }
 
-/* Prefill batches of 9..32 positions: Q4_K and Q6_K on the matrix cores. */
-#define QMV_FOR_M_WIDE(MACRO, FMT)                                                                     \
-    switch (m) {                                                                                       \
-    case 16: return MACRO(FMT, 16);                                                                    \
-    case 32: return MACRO(FMT, 32);                                                                    \
-    default: break;                                                                                    \
-    }
-
 #define QMV_LAUNCH(FMT, M) launch_matvec_fm<FMT, M>(p, grid, waves, s)
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
 {
     switch (fmt) {
-    case QMV_FMT_Q4_K:
-        QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K)
-        QMV_FOR_M_WIDE(QMV_LAUNCH, QMV_FMT_Q4_K)
-        break;
-    case QMV_FMT_Q6_K:
-        QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K)
-        QMV_FOR_M_WIDE(QMV_LAUNCH, QMV_FMT_Q6_K)
-        break;
+    case QMV_FMT_Q4_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K) break;
+    case QMV_FMT_Q6_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K) break;
     case QMV_FMT_Q8_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q8_0) break;
     case QMV_FMT_Q5_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q5_0) break;
     default: break;
@@ -1653,6 +1964,20 @@ hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, s, bval, bidx, bbad, nblocks, result);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(int fmt, const MatvecParams &p, int grid, hipStream_t s)
+{
+    switch (fmt) {
+    case QMV_FMT_Q4_K:
+        hipLaunchKernelGGL(prefill_kernel<QMV_FMT_Q4_K>, dim3(grid), dim3(QMV_PF_WAVES * 64), 0, s, p);
+        break;
+    case QMV_FMT_Q6_K:
+        hipLaunchKernelGGL(prefill_kernel<QMV_FMT_Q6_K>, dim3(grid), dim3(QMV_PF_WAVES * 64), 0, s, p);
+        break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -470,6 +470,26 @@ struct Epilogue {
     bool swiglu = false;               /* tensors (gate, up): out[0] = up * silu(gate) */
 };
 
+/* Prefill launches (9..32 positions): a workgroup takes QMV_PF_TILES tiles
+ * and a range of K-units. Measured on MI355X at Qwen2.5-7B layer shapes
+ * (M = 32): five units per split for long rows (down, 74 units: 82 us
+ * against 120 us at two) and for launches of many tile groups (gate|up, 148
+ * groups: 73 us against 103 us at two); two for small launches (q|k|v, o:
+ * 40 and 39 us against 51 at five), where more splits keep more CUs busy.
+ * units_per_wave, when forced, sets the units per split instead. */
+Plan plan_prefill(long long groups, int units)
+{
+    const int force_u = g_force_u.load();
+    int ups = force_u > 0 ? force_u : units >= 32 || groups >= 100 ? 5 : 2;
+    if (ups > units) ups = units;
+    Plan p;
+    p.units_per_wave = ups;
+    p.waves = QMV_PF_TILES;
+    p.units_per_split = ups;
+    p.splits = (units + ups - 1) / ups;
+    return p;
+}
+
 /* Enqueue one launch over `count` tensors sharing the input, for positions
  * [b0, b0 + batch) of the caller's batch (the caller's pointers are offset
  * here). */
@@ -477,17 +497,21 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
                  float *const *d_out, hipStream_t stream, Workspace &ws, const Epilogue &epi)
 {
     const QmvDeviceTensor *t0 = ts[0];
-    long long total_tiles = 0;
-    for (int i = 0; i < count; ++i) total_tiles += ts[i]->tiles;
-    const Plan plan = plan_for(total_tiles, t0->units);
     const bool mfma = use_matrix_cores(t0->geo.format, batch);
-    /* Kernel instance: exactly `batch` positions, or a 16 / 32 position
-     * matrix-core kernel with the batch in its first rows. */
-    const int mt = batch <= QMV_VALU_MAX_POSITIONS ? batch : batch <= 16 ? 16 : 32;
-    if (mt > QMV_VALU_MAX_POSITIONS && !mfma) {
+    /* Up to 8 positions: the matvec kernels for exactly `batch` positions.
+     * More: the prefill kernel, 32 position rows with the batch in the first. */
+    const bool prefill = batch > QMV_VALU_MAX_POSITIONS;
+    if (prefill && !mfma) {
         set_error("more than 8 positions per launch need the matrix-core path");
         return 0;
     }
+    const int mt = prefill ? QMV_MFMA_MAX_POSITIONS : batch;
+    long long total_tiles = 0, total_groups = 0;
+    for (int i = 0; i < count; ++i) {
+        total_tiles += ts[i]->tiles;
+        total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
+    }
+    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
@@ -520,7 +544,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
             partials += (size_t)ts[i]->tiles * plan.splits * mt * 64;
             counters += (size_t)ts[i]->tiles;
         }
-        wg += (long long)ts[i]->tiles * plan.splits;
+        wg += (long long)(prefill ? (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES : ts[i]->tiles) * plan.splits;
     }
     /* Fused SwiGLU: both projections' final tiles, then one count per tile
      * pair, after the split-K partials and counters. */
@@ -558,7 +582,10 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         p.argmax_result = epi.argmax;
         p.argmax_tiles = t0->tiles;
     }
-    HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, plan.waves, stream));
+    if (prefill)
+        HIP_TRY(qmv::launch_prefill(t0->geo.format, p, (int)wg, stream));
+    else
+        HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, plan.waves, stream));
     return 1;
 }
 

@@ -1,14 +1,15 @@
 """GPU parity of prefill batches of more than 8 positions (the reference
 prefills in chunks of QWEN2_PREFILL_CHUNK_SIZE = 8, src/qwen2_internal.h:7,
 through quantized_tensor_matmul_f32, src/quantized_matvec.cpp:164-224).
-Q4_K and Q6_K batches of 9..32 positions run as one launch on the matrix
-cores (position blocks of 16 sharing each decoded code tile); larger batches
-and the other formats run as consecutive launches.
+Q4_K and Q6_K batches of 9..32 positions run as one launch of the prefill
+kernel (four tiles per workgroup sharing activations staged in LDS, two
+position blocks of 16 per decoded code tile); larger batches and the other
+formats run as consecutive launches.
 
 Bars: every row of every position within 1e-5 * sum |w x| of the oracle;
-and, because a position's arithmetic on the matrix cores does not depend on
-the other positions of its launch, a wide launch is bit-identical to the
-same positions run in launches of at most 8 on the matrix cores.
+and, because a position's arithmetic in the prefill kernel does not depend
+on the other positions of its launch, a launch is bit-identical to the same
+positions run in smaller prefill launches.
 """
 import numpy as np
 import pytest
@@ -71,12 +72,12 @@ def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
 
 
 @pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K])
-@pytest.mark.parametrize("batch,parts", [(32, [8, 8, 8, 8]), (24, [8, 8, 8]), (12, [8, 4]), (20, [8, 8, 4]),
-                                         (9, [5, 4])])
-def test_wide_launch_bit_identical_to_narrow(qmv, gpu, hip, t, batch, parts):
-    """One launch of `batch` positions against the same positions in launches
-    of at most 8, all on the matrix cores (mfma_min_batch 1), on device
-    buffers."""
+@pytest.mark.parametrize("batch,parts", [(32, [16, 16]), (27, [9, 18]), (24, [12, 12]), (30, [10, 10, 10])])
+def test_prefill_positions_independent(qmv, gpu, hip, t, batch, parts):
+    """One prefill launch of `batch` positions against the same positions in
+    smaller prefill launches (each of 9 or more positions), on device
+    buffers: bit-identical, since a position's arithmetic does not depend on
+    the other positions of its launch."""
     rows, cols = 1000, 3584
     raw = qmv.synth_tensor(t, rows, cols, seed=320)
     dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
@@ -85,16 +86,12 @@ def test_wide_launch_bit_identical_to_narrow(qmv, gpu, hip, t, batch, parts):
     wide = hip.DeviceBuffer(4 * batch * rows)
     narrow = hip.DeviceBuffer(4 * batch * rows)
     s = hip.Stream()
-    qmv.set_launch_tuning(0, 0, 0, 1)
-    try:
-        dt.matvec(dx.ptr, batch, wide.ptr, s.handle)
-        b0 = 0
-        for n in parts:
-            dt.matvec(dx.ptr + 4 * b0 * cols, n, narrow.ptr + 4 * b0 * rows, s.handle)
-            b0 += n
-        s.synchronize()
-    finally:
-        qmv.set_launch_tuning(0, 0, 0, 0)
+    dt.matvec(dx.ptr, batch, wide.ptr, s.handle)
+    b0 = 0
+    for n in parts:
+        dt.matvec(dx.ptr + 4 * b0 * cols, n, narrow.ptr + 4 * b0 * rows, s.handle)
+        b0 += n
+    s.synchronize()
     assert np.array_equal(_bits(wide.to_array(np.float32, (batch, rows))),
                           _bits(narrow.to_array(np.float32, (batch, rows))))
     dt.close()
