@@ -1543,6 +1543,94 @@ __device__ __forceinline__ WgWork locate_pf(const MatvecParams &p, int wave)
     return w;
 }
 
+/* Prefill epilogue. A wave's tile values v(m) = val[m * 64 + lane] (m <
+ * npos) live in its LDS slice, and the loops over positions stay rolled:
+ * unrolled over 32 positions, the epilogue alone would be several times the
+ * instruction cache. Same split-K, addend and SwiGLU protocols (and the same
+ * partial order) as finish_tile / emit_tile. */
+typedef __attribute__((address_space(3))) float lds_f32;
+
+__device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, int lane, lds_f32 *val, int npos)
+{
+    const MatvecJob &job = p.job[w.job];
+    const int row = w.tile * 64 + lane;
+    const bool valid = row < job.rows;
+    if (job.add != nullptr && valid)
+        for (int m = 0; m < npos; ++m) val[m * 64 + lane] += job.add[(size_t)m * job.ldadd + row];
+    if (p.swiglu) {
+        const MatvecJob &out = p.job[0];
+        float *mine = p.pair_vals + ((size_t)w.job * out.tiles + w.tile) * QMV_PF_POS * 64 + lane;
+        for (int m = 0; m < npos; ++m) store_partial(mine + m * 64, val[m * 64 + lane]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(p.pair_count + w.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+        if (prev == 0u) return;
+        asm volatile("" ::: "memory");
+        const float *other = p.pair_vals + ((size_t)(1 - w.job) * out.tiles + w.tile) * QMV_PF_POS * 64 + lane;
+        for (int m0 = 0; m0 < npos; m0 += 8) {
+            float o[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = m0 + i < npos ? load_partial(other + (m0 + i) * 64) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (m0 + i >= npos) break;
+                const float v = val[(m0 + i) * 64 + lane];
+                const float g = w.job == 0 ? v : o[i];
+                const float u = w.job == 0 ? o[i] : v;
+                if (valid) out.y[(size_t)(m0 + i) * out.ldy + row] = swiglu_value(g, u);
+            }
+        }
+        if (lane == 0) __hip_atomic_store(p.pair_count + w.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (valid)
+        for (int m = 0; m < npos; ++m) job.y[(size_t)m * job.ldy + row] = val[m * 64 + lane];
+}
+
+__device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w, int lane, lds_f32 *val, int npos)
+{
+    const MatvecJob &job = p.job[w.job];
+    const int S = job.splits;
+    if (S > 1) {
+        float *part = p.partials + job.partial_offset + ((size_t)w.tile * S) * QMV_PF_POS * 64 + lane;
+        unsigned *count = p.counters + job.counter_offset + w.tile;
+        for (int m = 0; m < npos; ++m) store_partial(part + ((size_t)w.split * QMV_PF_POS + m) * 64, val[m * 64 + lane]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+        if (prev != (unsigned)S - 1u) return;
+        asm volatile("" ::: "memory");
+        /* Eight positions x eight splits of loads in flight; each position
+         * is summed in split order, as sum_partials does. */
+        for (int m0 = 0; m0 < npos; m0 += 8) {
+            float sum[8];
+            for (int s0 = 0; s0 < S; s0 += 8) {
+                float v[8][8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        v[i][k] = m0 + i < npos && s0 + k < S
+                                      ? load_partial(part + ((size_t)(s0 + k) * QMV_PF_POS + m0 + i) * 64)
+                                      : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        if (s0 + k < S) sum[i] = s0 + k == 0 ? v[i][k] : sum[i] + v[i][k];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (m0 + i < npos) val[(m0 + i) * 64 + lane] = sum[i];
+        }
+        if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    pf_emit(p, w, lane, val, npos);
+}
+
 template <int FMT>
 __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams p)
 {
@@ -1613,15 +1701,15 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
     /* Each wave transposes its tile through its own slice of the (now free)
      * staging buffer, then finishes the tile on its own. */
     __syncthreads();
-    float(*red)[QMV_PF_POS][64] = reinterpret_cast<float(*)[QMV_PF_POS][64]>(lds_buf) + wave;
+    lds_f32 *val = (lds_f32 *)lds + wave * QMV_PF_POS * 64;
 #pragma unroll
     for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) red[0][16 * pb + 4 * kc + j][16 * g + n] = acc[pb][g][j];
+            for (int j = 0; j < 4; ++j) val[(16 * pb + 4 * kc + j) * 64 + 16 * g + n] = acc[pb][g][j];
     if (!active) return;
-    finish_tile<QMV_PF_POS>(p, w, 1, lane, red, npos);
+    pf_finish(p, w, lane, val, npos);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------

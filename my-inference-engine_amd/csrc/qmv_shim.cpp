@@ -472,10 +472,10 @@ struct Epilogue {
 
 /* Prefill launches (9..32 positions): a workgroup takes QMV_PF_TILES tiles
  * and a range of K-units. Measured on MI355X at Qwen2.5-7B layer shapes
- * (M = 32): five units per split for long rows (down, 74 units: 82 us
- * against 120 us at two) and for launches of many tile groups (gate|up, 148
- * groups: 73 us against 103 us at two); two for small launches (q|k|v, o:
- * 40 and 39 us against 51 at five), where more splits keep more CUs busy.
+ * (M = 32): five units per split for long rows (down, 74 units: 74 us
+ * against 100 us at two) and for launches of many tile groups (gate|up, 148
+ * groups: 64 us against 77 us at two); two for small launches (q|k|v, o:
+ * 28 and 27 us against 41 at five), where more splits keep more CUs busy.
  * units_per_wave, when forced, sets the units per split instead. */
 Plan plan_prefill(long long groups, int units)
 {
