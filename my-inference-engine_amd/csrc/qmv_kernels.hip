@@ -924,26 +924,23 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
         sum[m] = s;
     }
 
-    if (job.splits == 1) {
-        emit_tile<M>(p, w, lane, npos, sum);
-        return;
+    if (job.splits > 1) {
+        float *part = p.partials + job.partial_offset + ((size_t)w.tile * job.splits) * M * 64;
+        unsigned *count = p.counters + job.counter_offset + w.tile;
+#pragma unroll
+        for (int m = 0; m < M; ++m) store_partial(part + ((size_t)w.split * M + m) * 64 + lane, sum[m]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+        if (prev != (unsigned)job.splits - 1u) return;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < M; ++m) sum[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
+        if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-
-    float *part = p.partials + job.partial_offset + ((size_t)w.tile * job.splits) * M * 64;
-    unsigned *count = p.counters + job.counter_offset + w.tile;
-#pragma unroll
-    for (int m = 0; m < M; ++m) store_partial(part + ((size_t)w.split * M + m) * 64 + lane, sum[m]);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
-    if (prev != (unsigned)job.splits - 1u) return;
-    asm volatile("" ::: "memory");
-    float fin[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) fin[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
-    if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    emit_tile<M>(p, w, lane, npos, fin);
+    /* One copy of the row epilogue serves both paths. */
+    emit_tile<M>(p, w, lane, npos, sum);
 }
 
 /* kOne: every wave takes at most one unit (units_per_wave == 1), so no
