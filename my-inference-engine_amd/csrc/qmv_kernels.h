@@ -76,9 +76,9 @@ hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, f
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
                          int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
                          hipStream_t s);
-/* Prefill launch (Q4_K / Q6_K, 9..32 positions): grid = sum over jobs of
- * ceil(tiles / 4) tile groups x splits. */
-hipError_t launch_prefill(int fmt, const MatvecParams &p, int grid, hipStream_t s);
+/* Prefill launch (Q4_K / Q6_K, up to `rows` = 16 or 32 positions): grid =
+ * sum over jobs of ceil(tiles / 4) tile groups x splits. */
+hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s);
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out,
                            hipStream_t s);
 hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,

@@ -1252,7 +1252,7 @@ matvec_mfma_kernel(MatvecParams p)
  * the matrix-core section above) laid out in MFMA A-fragment order, and each
  * wave then runs its tile's unit with A read from LDS: an activation is
  * loaded and split once per workgroup instead of once per wave, and the
- * codes a wave decodes serve both position blocks of 16. The next unit's
+ * codes a wave decodes serve every position block of 16. The next unit's
  * activations are loaded into registers, and its weight headers and first
  * codes issued, while the current unit computes. Each wave finishes its own
  * tile with the split-K protocol of finish_tile, so a position's arithmetic
@@ -1266,7 +1266,8 @@ matvec_mfma_kernel(MatvecParams p)
 #ifndef QMV_PF_NEXT_T
 #define QMV_PF_NEXT_T 13
 #endif
-#define QMV_PF_POS 32
+/* A prefill launch carries P position blocks of 16 (P = 1 for up to 16
+ * positions, 2 for up to 32). */
 
 /* The staging buffer is addressed through an explicit LDS pointer type so
  * that every access compiles to ds_read / ds_write. */
@@ -1283,20 +1284,21 @@ __device__ __forceinline__ int lds_off_after(int off, float dep)
 /* LDS image of one unit: fragment (limb L, position block pb, k-block b) is
  * 64 lanes x KL bf16, lane 16 kc + n holding A[n][KL kc .. KL kc + KL - 1] =
  * limb L of x[16 pb + n][4 KL b + KL kc ..]. */
-template <int KL> struct PfLayout {
+template <int KL, int P> struct PfLayout {
     static constexpr int kBlocks = 256 / (4 * KL);     /* 8 (Q4_K) or 16 (Q6_K) */
     static constexpr int kFrag = 64 * 2 * KL;          /* bytes per fragment */
-    static constexpr int kChunks = 2 * kBlocks * 64;   /* (pb, b, lane) chunks of KL activations */
+    static constexpr int kChunks = P * kBlocks * 64;   /* (pb, b, lane) chunks of KL activations */
     static constexpr int kPerThread = kChunks / (QMV_PF_WAVES * 64);
-    static constexpr int kBytes = 3 * 2 * kBlocks * kFrag; /* 48 KB */
-    __device__ static int offset(int limb, int pb, int b) { return ((limb * 2 + pb) * kBlocks + b) * kFrag; }
+    static constexpr int kBytes = 3 * P * kBlocks * kFrag; /* 24 KB per position block */
+    __device__ static int offset(int limb, int pb, int b) { return ((limb * P + pb) * kBlocks + b) * kFrag; }
 };
 
 /* Chunk c of a unit: lane = c % 64, block b, position block pb. */
-template <int KL>
-__device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, int tid, float (&xr)[PfLayout<KL>::kPerThread][KL])
+template <int KL, int P>
+__device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, int tid,
+                                          float (&xr)[PfLayout<KL, P>::kPerThread][KL])
 {
-    using L = PfLayout<KL>;
+    using L = PfLayout<KL, P>;
 #pragma unroll
     for (int i = 0; i < L::kPerThread; ++i) {
         const int c = tid + i * QMV_PF_WAVES * 64;
@@ -1312,10 +1314,10 @@ __device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, in
     }
 }
 
-template <int KL>
-__device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid, const float (&xr)[PfLayout<KL>::kPerThread][KL])
+template <int KL, int P>
+__device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid, const float (&xr)[PfLayout<KL, P>::kPerThread][KL])
 {
-    using L = PfLayout<KL>;
+    using L = PfLayout<KL, P>;
     typedef __bf16 frag_t __attribute__((__vector_size__(KL * sizeof(__bf16))));
 #pragma unroll
     for (int i = 0; i < L::kPerThread; ++i) {
@@ -1334,10 +1336,11 @@ __device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid, const float
  * hold the unit's headers and group-0 codes on entry and those of `next` on
  * return (the caller passes the unit itself when there is no next one: the
  * loads are then harmless repeats, and no branch splits the unrolled body). */
+template <int P>
 __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
-                                            f32x4_t (&acc)[2][4], uint4 (&h)[4], uint2 (&q0)[4])
+                                            f32x4_t (&acc)[P][4], uint4 (&h)[4], uint2 (&q0)[4])
 {
-    using L = PfLayout<8>;
+    using L = PfLayout<8, P>;
     const int kc = lane >> 4, n = lane & 15;
     const int qoff = (1 + (kc >> 1)) * 1024 + n * 16 + 8 * (kc & 1);
     const uint8_t *qsp = slab + qoff;
@@ -1379,7 +1382,7 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
         }
         float sa[4], sm[4];
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
+        for (int pb = 0; pb < P; ++pb) {
             typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
             const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
             const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, sb));
@@ -1433,11 +1436,12 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
 
 /* Q6_K: sc, dg and w0 (the first (G, hf) pair's words) hold this unit's on
  * entry and those of `next` on return (as for Q4_K). */
+template <int P>
 __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
-                                            f32x4_t (&acc)[2][4], uint4 (&sc)[4], uint32_t (&dgw)[4],
+                                            f32x4_t (&acc)[P][4], uint4 (&sc)[4], uint32_t (&dgw)[4],
                                             uint32_t (&w0)[4][3])
 {
-    using L = PfLayout<4>;
+    using L = PfLayout<4, P>;
     const int kc = lane >> 4, n = lane & 15;
     const int woff = n * 16 + 4 * kc;
     const uint8_t *wp = slab + woff;
@@ -1488,7 +1492,7 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
         }
         float s[4];
 #pragma unroll
-        for (int pb = 0; pb < 2; ++pb) {
+        for (int pb = 0; pb < P; ++pb) {
             typedef __attribute__((address_space(3))) const bf16x4_t lds_a;
             const lds_u8 *la = lds + lds_off_after(lane * 8, acc[pb][3][3]);
             const bf16x4_t a0 = *(lds_a *)(la + L::offset(0, pb, j));
@@ -1547,6 +1551,7 @@ __device__ __forceinline__ WgWork locate_pf(const MatvecParams &p, int wave)
  * partial order) as finish_tile / emit_tile. */
 typedef __attribute__((address_space(3))) float lds_f32;
 
+template <int MP>
 __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, int lane, lds_f32 *val, int npos)
 {
     const MatvecJob &job = p.job[w.job];
@@ -1556,7 +1561,7 @@ __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, 
         for (int m = 0; m < npos; ++m) val[m * 64 + lane] += job.add[(size_t)m * job.ldadd + row];
     if (p.swiglu) {
         const MatvecJob &out = p.job[0];
-        float *mine = p.pair_vals + ((size_t)w.job * out.tiles + w.tile) * QMV_PF_POS * 64 + lane;
+        float *mine = p.pair_vals + ((size_t)w.job * out.tiles + w.tile) * MP * 64 + lane;
         for (int m = 0; m < npos; ++m) store_partial(mine + m * 64, val[m * 64 + lane]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned prev = 0;
@@ -1565,7 +1570,7 @@ __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, 
         prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
         if (prev == 0u) return;
         asm volatile("" ::: "memory");
-        const float *other = p.pair_vals + ((size_t)(1 - w.job) * out.tiles + w.tile) * QMV_PF_POS * 64 + lane;
+        const float *other = p.pair_vals + ((size_t)(1 - w.job) * out.tiles + w.tile) * MP * 64 + lane;
         for (int m0 = 0; m0 < npos; m0 += 8) {
             float o[8];
 #pragma unroll
@@ -1586,14 +1591,15 @@ __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, 
         for (int m = 0; m < npos; ++m) job.y[(size_t)m * job.ldy + row] = val[m * 64 + lane];
 }
 
+template <int MP>
 __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w, int lane, lds_f32 *val, int npos)
 {
     const MatvecJob &job = p.job[w.job];
     const int S = job.splits;
     if (S > 1) {
-        float *part = p.partials + job.partial_offset + ((size_t)w.tile * S) * QMV_PF_POS * 64 + lane;
+        float *part = p.partials + job.partial_offset + ((size_t)w.tile * S) * MP * 64 + lane;
         unsigned *count = p.counters + job.counter_offset + w.tile;
-        for (int m = 0; m < npos; ++m) store_partial(part + ((size_t)w.split * QMV_PF_POS + m) * 64, val[m * 64 + lane]);
+        for (int m = 0; m < npos; ++m) store_partial(part + ((size_t)w.split * MP + m) * 64, val[m * 64 + lane]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned prev = 0;
         if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1611,7 +1617,7 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
 #pragma unroll
                     for (int k = 0; k < 8; ++k)
                         v[i][k] = m0 + i < npos && s0 + k < S
-                                      ? load_partial(part + ((size_t)(s0 + k) * QMV_PF_POS + m0 + i) * 64)
+                                      ? load_partial(part + ((size_t)(s0 + k) * MP + m0 + i) * 64)
                                       : 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
@@ -1625,16 +1631,17 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
         }
         if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    pf_emit(p, w, lane, val, npos);
+    pf_emit<MP>(p, w, lane, val, npos);
 }
 
-template <int FMT>
+template <int FMT, int P>
 __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams p)
 {
     constexpr int KL = FMT == QMV_FMT_Q4_K ? 8 : 4;
     constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
-    using L = PfLayout<KL>;
-    static_assert(QMV_PF_WAVES * QMV_PF_POS * 64 * 4 <= L::kBytes, "combine buffer reuses the staging buffer");
+    constexpr int MP = 16 * P; /* position rows of the launch */
+    using L = PfLayout<KL, P>;
+    static_assert(QMV_PF_WAVES * MP * 64 * 4 <= L::kBytes, "combine buffer reuses the staging buffer");
     __shared__ __attribute__((aligned(16))) uint8_t lds_buf[L::kBytes];
     lds_u8 *lds = (lds_u8 *)lds_buf;
 
@@ -1648,9 +1655,9 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
     const uint8_t *wtile = job.w + (size_t)(active ? w.tile : 0) * p.units * SLAB;
     const int kc = lane >> 4, n = lane & 15;
 
-    f32x4_t acc[2][4];
+    f32x4_t acc[P][4];
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+    for (int pb = 0; pb < P; ++pb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) acc[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -1678,35 +1685,35 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
         }
     }
     float xr[L::kPerThread][KL];
-    pf_load_x<KL>(p.x + (size_t)w.u_begin * 256, p.ldx, npos, tid, xr);
+    pf_load_x<KL, P>(p.x + (size_t)w.u_begin * 256, p.ldx, npos, tid, xr);
 
     for (int u = w.u_begin; u < w.u_end; ++u) {
         __syncthreads(); /* every wave is done with the previous unit's image */
-        pf_store_limbs<KL>(lds, tid, xr);
+        pf_store_limbs<KL, P>(lds, tid, xr);
         __syncthreads();
-        if (u + 1 < w.u_end) pf_load_x<KL>(p.x + (size_t)(u + 1) * 256, p.ldx, npos, tid, xr);
+        if (u + 1 < w.u_end) pf_load_x<KL, P>(p.x + (size_t)(u + 1) * 256, p.ldx, npos, tid, xr);
         const uint8_t *slab = wtile + (size_t)u * SLAB;
         const uint8_t *next = u + 1 < w.u_end ? slab + SLAB : slab;
         if (active) {
             if constexpr (FMT == QMV_FMT_Q4_K)
-                q4k_unit_pf(slab, next, lds, lane, acc, h, q0);
+                q4k_unit_pf<P>(slab, next, lds, lane, acc, h, q0);
             else
-                q6k_unit_pf(slab, next, lds, lane, acc, h, dgw, w0);
+                q6k_unit_pf<P>(slab, next, lds, lane, acc, h, dgw, w0);
         }
     }
 
     /* Each wave transposes its tile through its own slice of the (now free)
      * staging buffer, then finishes the tile on its own. */
     __syncthreads();
-    lds_f32 *val = (lds_f32 *)lds + wave * QMV_PF_POS * 64;
+    lds_f32 *val = (lds_f32 *)lds + wave * MP * 64;
 #pragma unroll
-    for (int pb = 0; pb < 2; ++pb)
+    for (int pb = 0; pb < P; ++pb)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int j = 0; j < 4; ++j) val[(16 * pb + 4 * kc + j) * 64 + 16 * g + n] = acc[pb][g][j];
     if (!active) return;
-    pf_finish(p, w, lane, val, npos);
+    pf_finish<MP>(p, w, lane, val, npos);
 }
 
 /* ---- dequantisation kernel --------------------------------------------------
@@ -2052,17 +2059,14 @@ hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int fmt, const MatvecParams &p, int grid, hipStream_t s)
+hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s)
 {
-    switch (fmt) {
-    case QMV_FMT_Q4_K:
-        hipLaunchKernelGGL(prefill_kernel<QMV_FMT_Q4_K>, dim3(grid), dim3(QMV_PF_WAVES * 64), 0, s, p);
-        break;
-    case QMV_FMT_Q6_K:
-        hipLaunchKernelGGL(prefill_kernel<QMV_FMT_Q6_K>, dim3(grid), dim3(QMV_PF_WAVES * 64), 0, s, p);
-        break;
-    default: return hipErrorInvalidValue;
-    }
+    const dim3 g(grid), b(QMV_PF_WAVES * 64);
+    if (fmt == QMV_FMT_Q4_K && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q4_K, 1>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q4_K && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q4_K, 2>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q6_K && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q6_K, 1>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q6_K && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q6_K, 2>), g, b, 0, s, p);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

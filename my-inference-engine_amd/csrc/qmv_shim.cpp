@@ -499,13 +499,14 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const QmvDeviceTensor *t0 = ts[0];
     const bool mfma = use_matrix_cores(t0->geo.format, batch);
     /* Up to 8 positions: the matvec kernels for exactly `batch` positions.
-     * More: the prefill kernel, 32 position rows with the batch in the first. */
+     * More: the prefill kernel, 16 or 32 position rows with the batch in the
+     * first. */
     const bool prefill = batch > QMV_VALU_MAX_POSITIONS;
     if (prefill && !mfma) {
         set_error("more than 8 positions per launch need the matrix-core path");
         return 0;
     }
-    const int mt = prefill ? QMV_MFMA_MAX_POSITIONS : batch;
+    const int mt = !prefill ? batch : batch <= 16 ? 16 : QMV_MFMA_MAX_POSITIONS;
     long long total_tiles = 0, total_groups = 0;
     for (int i = 0; i < count; ++i) {
         total_tiles += ts[i]->tiles;
@@ -583,7 +584,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         p.argmax_tiles = t0->tiles;
     }
     if (prefill)
-        HIP_TRY(qmv::launch_prefill(t0->geo.format, p, (int)wg, stream));
+        HIP_TRY(qmv::launch_prefill(t0->geo.format, p, mt, (int)wg, stream));
     else
         HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, plan.waves, stream));
     return 1;
