@@ -18,9 +18,10 @@ kernel and workload, and the CPU baseline (the reference's own x86 build,
 AVX2 + OpenMP, on a bounded sample). `extra` adds the same set at M=8 and at
 M=32 (a prefill chunk of 32 positions per pass over the weights), the
 per-step p10/p50/p90, eager (ungraphed) launch time, a measured streaming
-read bandwidth, the vocabulary projection with greedy sampling, and the same
+read bandwidth, the vocabulary projection with greedy sampling, the same
 layers as a device-resident decode step with its element operations
-(biases, residuals, RMSNorm, SwiGLU).
+(biases, residuals, RMSNorm, SwiGLU), and the small Qwen2.5-0.5B/1.5B
+configurations (cold and warm).
 """
 import argparse
 import ctypes
@@ -301,6 +302,53 @@ def decode_ops_bench(qmv, hip, stream, layers, reps):
     return out
 
 
+def small_configs_bench(qmv, hip, stream, reps):
+    """The small reference configurations, latency- and launch-bound:
+    Q8_0 896x896 (Qwen2.5-0.5B q_proj) and Q6_K 896x4864 (its FFN down; the
+    Q4_K 4864x896 gate/up shape is not a valid Q4_K tensor and is rejected,
+    as by the reference) at M=1, and one Qwen2.5-1.5B layer set at M=8 (q|k|v
+    Q5_0 1536/256/256x1536, o Q5_0 1536x1536, gate|up Q4_K 8960x1536, down
+    Q4_K 1536x8960) as its four launches. Cold: graph replays cycling through
+    enough copies to exceed 1 GB (twice the Infinity Cache); warm: one copy."""
+    Q5_0, Q8_0 = 6, 8
+    D = hip.DeviceBuffer
+    sp = stream.handle
+    cases = {
+        "q8_0_896x896_m1": (1, [[("a", Q8_0, 896, 896)]]),
+        "q6_k_896x4864_m1": (1, [[("a", Q6_K, 896, 4864)]]),
+        "qwen2_1_5b_layer_set_m8": (8, [[("q", Q5_0, 1536, 1536), ("k", Q5_0, 256, 1536), ("v", Q5_0, 256, 1536)],
+                                        [("o", Q5_0, 1536, 1536)],
+                                        [("gate", Q4_K, 8960, 1536), ("up", Q4_K, 8960, 1536)],
+                                        [("down", Q4_K, 1536, 8960)]]),
+    }
+    out = {}
+    for name, (m, groups) in cases.items():
+        raws = {t[0]: qmv.synth_tensor(t[1], t[2], t[3], seed=900 + i)
+                for i, t in enumerate(x for g in groups for x in g)}
+        nbytes = sum(r.size for r in raws.values())
+        copies = max(2, -(-(1 << 30) // nbytes))
+        sets = [{t[0]: qmv.DeviceTensor(qmv.make_view(raws[t[0]], t[1], t[2], t[3])) for g in groups for t in g}
+                for _ in range(copies)]
+        xs = [D.from_array(qmv.synth_normal(m * g[0][3], seed=950 + j)) for j, g in enumerate(groups)]
+        ys = [[D(4 * m * t[2]) for t in g] for g in groups]
+
+        def launches(ts):
+            return [lambda g=g, x=x, y=y: qmv.device_matvec_group([ts[t[0]] for t in g], x.ptr, m,
+                                                                  [b.ptr for b in y], sp)
+                    for g, x, y in zip(groups, xs, ys)]
+
+        cold = graph_us(hip, stream, [fn for ts in sets for fn in launches(ts)], reps) / copies
+        # Warm: the first copy's launches repeated as many times in one graph.
+        warm = graph_us(hip, stream, launches(sets[0]) * copies, reps) / copies
+        out[name] = {"packed_bytes": nbytes, "launches": len(groups), "positions": m, "copies_cold": copies,
+                     "cold_us": round(cold, 2), "warm_us": round(warm, 2),
+                     "cold_weight_gbs": round(nbytes / (cold * 1e-6) / 1e9, 1)}
+        for ts in sets:
+            for d in ts.values():
+                d.close()
+    return out
+
+
 def committed_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
     summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by a copy-kernel
@@ -408,6 +456,7 @@ def main():
             ops["projection_set_ms"] = round(main_run["ms_per_step"], 4)
             ops["element_ops_overhead_ms"] = round(ops["ms_per_step"] - main_run["ms_per_step"], 4)
             extra["decode_step_with_element_ops"] = ops
+        extra["small_configs"] = small_configs_bench(qmv, hip, stream, max(5, args.steps // 10))
         probe = importlib.import_module("my-inference-engine_amd.probe")
         extra["hbm_read_probe"] = probe.read_bandwidth(1 << 30, 512, 10)
         extra["hbm_fraction_of_read_probe"] = round(value / extra["hbm_read_probe"]["gbs"], 4)
