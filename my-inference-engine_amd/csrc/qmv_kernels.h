@@ -79,6 +79,8 @@ hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, in
 /* Prefill launch (Q4_K / Q6_K, up to `rows` = 16 or 32 positions): grid =
  * sum over jobs of ceil(tiles / 4) tile groups x splits. */
 hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s);
+/* Plain fp32 copy (n elements) as a kernel, e.g. from mapped host memory. */
+hipError_t launch_copy(const float *src, float *dst, size_t n, hipStream_t s);
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out,
                            hipStream_t s);
 hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,

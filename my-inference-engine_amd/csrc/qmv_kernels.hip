@@ -2070,6 +2070,19 @@ hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hi
     return hipGetLastError();
 }
 
+__global__ void __launch_bounds__(256) copy_f32_kernel(const float *__restrict__ src, float *__restrict__ dst, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy(const float *src, float *dst, size_t n, hipStream_t s)
+{
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(copy_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out, hipStream_t s)
 {
     hipLaunchKernelGGL(rms_norm_kernel, dim3(batch), dim3(QMV_NORM_THREADS), 0, s, x, w, n, eps, out);

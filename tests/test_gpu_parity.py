@@ -374,22 +374,25 @@ def hip(qmv):
     return importlib.import_module("my-inference-engine_amd.hip_runtime")
 
 
-def test_device_api_matches_host_api(qmv, gpu, hip):
-    t, rows, cols = B.Q4_K, 18944, 3584
+@pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 18944, 3584), (B.Q6_K, 3584, 18944)])
+def test_device_api_matches_host_api(qmv, gpu, hip, t, rows, cols):
+    """The host-pointer drop-in (input copied in, or for 32 KB and more read
+    by a copy kernel; output written by the kernels into pinned memory) gives
+    the device API's bits, at M = 1, 8 and 32."""
     raw = qmv.synth_tensor(t, rows, cols, seed=21)
     v = qmv.make_view(raw, t, rows, cols)
     dt = qmv.DeviceTensor(v)
     assert (dt.rows, dt.cols, dt.packed_bytes) == (rows, cols, raw.size)
-    x = qmv.synth_normal(8 * cols, seed=22).reshape(8, cols)
+    x = qmv.synth_normal(32 * cols, seed=22).reshape(32, cols)
     dx = hip.DeviceBuffer.from_array(x)
-    dy = hip.DeviceBuffer(8 * rows * 4)
+    dy = hip.DeviceBuffer(32 * rows * 4)
     stream = hip.Stream()
-    for m in (1, 8):
+    for m in (1, 8, 32):
         dt.matvec(dx.ptr, m, dy.ptr, stream.handle)
         stream.synchronize()
         host = qmv.matvec(v, x[:m] if m > 1 else x[0]).reshape(m, rows)
-        got = dy.to_array(np.float32, (8, rows))[:m]
-        assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
+        got = dy.to_array(np.float32, (32, rows))[:m]
+        assert np.array_equal(got.view(np.uint32), host.view(np.uint32)), m
     out = hip.DeviceBuffer(5 * cols * 4)
     dt.dequantize(100, 5, out.ptr, stream.handle)
     stream.synchronize()
