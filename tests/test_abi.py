@@ -138,6 +138,16 @@ def test_rms_norm_argument_table_without_gpu(qmv):
     assert (buf == 0).all()
 
 
+def test_cxx_dropin_argument_table_without_gpu(qmv):
+    """The reference's C++ entry points, called from a C++ program built
+    against include/quantized_matvec.h, reject the invalid-argument table
+    before any device work (tests/cxx/dropin_test.cpp)."""
+    exe = os.path.join(ROOT, "tests", "cxx", "dropin_test")
+    assert os.path.exists(exe), "tests/cxx/dropin_test missing: run __graft_entry__.build()"
+    r = subprocess.run([exe, "--args"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 def test_synth_is_deterministic_and_distributed(qmv):
     a = qmv.synth_tensor(B.Q4_K, 64, 512, seed=5)
     b = qmv.synth_tensor(B.Q4_K, 64, 512, seed=5)

@@ -368,6 +368,18 @@ def test_cache_follows_new_contents(qmv, gpu):
     qmv.release_all()
 
 
+def test_cxx_dropin_program(qmv, gpu):
+    """The drop-in from C++ (tests/cxx/dropin_test.cpp): quantized_tensor_
+    matvec_f32 / _matmul_f32 with their original signatures on all four
+    formats, M = 1 to 40, each row within tolerance of the oracle."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cxx", "dropin_test")
+    assert os.path.exists(exe), "tests/cxx/dropin_test missing: run __graft_entry__.build()"
+    log("running tests/cxx/dropin_test")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
 @pytest.fixture(scope="module")
 def hip(qmv):
     import importlib
