@@ -164,3 +164,44 @@ def test_device_batch_limit(qmv, gpu, hip):
     with pytest.raises(qmv.QmvError):
         dt.matvec(dx.ptr, 33, dy.ptr, 0)
     dt.close()
+
+
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K])
+@pytest.mark.parametrize("rows,cols,batch", [(1, 256, 9), (63, 512, 32), (130, 256, 17), (65, 2304, 12),
+                                             (257, 1024, 31)])
+def test_prefill_edge_shapes(qmv, oracle, gpu, t, rows, cols, batch):
+    """Tile groups with idle waves (1, 2 or 3 of 4 tiles real), partial last
+    tiles, a single K-unit, and odd position counts."""
+    raw = qmv.synth_tensor(t, rows, cols, seed=360 + rows)
+    x = qmv.synth_normal(batch * cols, seed=361 + rows).reshape(batch, cols)
+    v = qmv.make_view(raw, t, rows, cols)
+    y = qmv.matvec(v, x)
+    _check(oracle, raw, t, rows, cols, x, y, f"type {t} {rows}x{cols} B={batch}")
+    qmv.release_tensor(v.data)
+
+
+def test_prefill_group_with_biases(qmv, oracle, gpu, hip):
+    """q/k/v of different row counts in one prefill launch (jobs with 6, 1
+    and 1 tile groups), each with its bias, at 24 positions."""
+    t, cols, batch = B.Q4_K, 1536, 24
+    shapes = [1536, 256, 256]
+    raws = [qmv.synth_tensor(t, r, cols, seed=370 + i) for i, r in enumerate(shapes)]
+    dts = [qmv.DeviceTensor(qmv.make_view(raw, t, r, cols)) for raw, r in zip(raws, shapes)]
+    x = qmv.synth_normal(batch * cols, seed=373).reshape(batch, cols)
+    dx = hip.DeviceBuffer.from_array(x)
+    rng = np.random.default_rng(374)
+    biases = [rng.standard_normal(r).astype(np.float32) for r in shapes]
+    dbs = [hip.DeviceBuffer.from_array(b) for b in biases]
+    plain = [hip.DeviceBuffer(4 * batch * r) for r in shapes]
+    biased = [hip.DeviceBuffer(4 * batch * r) for r in shapes]
+    s = hip.Stream()
+    qmv.device_matvec_group(dts, dx.ptr, batch, [o.ptr for o in plain], s.handle)
+    qmv.device_matvec_add_group(dts, dx.ptr, batch, [b.ptr for b in dbs], [0, 0, 0], [o.ptr for o in biased],
+                                s.handle)
+    s.synchronize()
+    for raw, r, p_, b_, bias in zip(raws, shapes, plain, biased, biases):
+        yp = p_.to_array(np.float32, (batch, r))
+        _check(oracle, raw, t, r, cols, x, yp, f"group rows {r} B={batch}")
+        assert np.array_equal(_bits(b_.to_array(np.float32, (batch, r))), _bits(yp + bias[None, :]))
+    for d in dts:
+        d.close()
