@@ -86,8 +86,10 @@ def cpu_baseline(qmv, host_layer, batch, seconds):
 
 def kernel_name(fmt, M):
     """The kernel a Q4_K / Q6_K launch of M positions runs (default tuning)."""
+    if M > 8:
+        return "prefill_kernel<%s,%d>" % (fmt, 1 if M <= 16 else 2)
     if M >= (7 if fmt == "Q4_K" else 8):
-        return "matvec_mfma_kernel<%s,%d>" % (fmt, M if M <= 8 else 16 if M <= 16 else 32)
+        return "matvec_mfma_kernel<%s,%d>" % (fmt, M)
     return "matvec_kernel<%s,%d>" % (fmt, M)
 
 
