@@ -50,6 +50,30 @@ def layer_shapes():
             ("down", Q6_K, HIDDEN, INTER)]
 
 
+def _cpu_layer(qmv, host_layer, batch):
+    import oracle
+
+    views, xs, ys, nbytes = [], [], [], 0
+    for name, t, rows, cols, raw in host_layer:
+        views.append((oracle.view(raw, t, rows, cols), rows, cols))
+        xs.append(qmv.synth_normal(batch * cols, seed=7000 + cols))
+        ys.append(np.empty(batch * rows, dtype=np.float32))
+        nbytes += raw.size
+    return views, xs, ys, nbytes
+
+
+def _time_cpu(fn, views, xs, ys, batch, seconds):
+    """Median seconds per pass over layer 0's seven matvecs, ~`seconds` of passes."""
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        for (v, rows, cols), x, y in zip(views, xs, ys):
+            assert fn(ctypes.byref(v), x.ctypes.data, cols, batch, y.ctypes.data, rows) == 1
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(qmv, host_layer, batch, seconds):
     """Time the reference's CPU path (its own sources, x86 Release flags with
     AVX2/FMA/F16C and OpenMP) on layer 0's seven matvecs for ~`seconds`."""
@@ -61,27 +85,36 @@ def cpu_baseline(qmv, host_layer, batch, seconds):
         kind, lib = "port", oracle.lib()
     fn = lib.ref_quantized_tensor_matmul_f32 if kind == "reference" else lib.oracle_matmul_f32
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-    views, xs, ys, nbytes = [], [], [], 0
-    for name, t, rows, cols, raw in host_layer:
-        v = oracle.view(raw, t, rows, cols)
-        x = qmv.synth_normal(batch * cols, seed=7000 + cols)
-        views.append((v, rows, cols))
-        xs.append(x)
-        ys.append(np.empty(batch * rows, dtype=np.float32))
-        nbytes += raw.size
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        for (v, rows, cols), x, y in zip(views, xs, ys):
-            assert fn(ctypes.byref(v), x.ctypes.data, cols, batch, y.ctypes.data, rows) == 1
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    views, xs, ys, nbytes = _cpu_layer(qmv, host_layer, batch)
+    med, reps = _time_cpu(fn, views, xs, ys, batch, seconds)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": f"layer 0 of the set (7 matvecs, {nbytes} packed bytes, M={batch}), "
-                      f"{len(times)} repetitions, median {med * 1e3:.1f} ms "
+                      f"{reps} repetitions, median {med * 1e3:.1f} ms "
                       f"({'oracle/_ref/libref_avx2.so: -O3 -mavx2 -mfma -mf16c -fopenmp' if kind == 'reference' else 'oracle/liboracle.so scalar port'}, "
                       f"OMP_NUM_THREADS={threads})"}
+
+
+def cpu_variants(qmv, host_layer, batch, seconds):
+    """The other CPU figures on the same layer: the reference's AVX2 build on
+    one thread, and the scalar restatement (oracle, -O2 with no SIMD flags) on
+    all threads; GB/s each."""
+    import oracle
+
+    views, xs, ys, nbytes = _cpu_layer(qmv, host_layer, batch)
+    out = {}
+    ref = oracle.ref_lib("avx2")
+    if ref is not None:
+        gomp = ctypes.CDLL("libgomp.so.1")
+        before = gomp.omp_get_max_threads()
+        gomp.omp_set_num_threads(1)
+        try:
+            med, _ = _time_cpu(ref.ref_quantized_tensor_matmul_f32, views, xs, ys, batch, seconds)
+        finally:
+            gomp.omp_set_num_threads(before)
+        out["reference_avx2_1_thread_gbs"] = round(nbytes / med / 1e9, 3)
+    med, _ = _time_cpu(oracle.lib().oracle_matmul_f32, views, xs, ys, batch, seconds)
+    out["scalar_port_all_threads_gbs"] = round(nbytes / med / 1e9, 3)
+    return out
 
 
 def kernel_name(fmt, M):
@@ -486,6 +519,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(qmv, host_layer0, M, args.cpu_seconds)
+        if not args.no_extra:
+            extra["cpu_variants"] = cpu_variants(qmv, host_layer0, M, min(3.0, args.cpu_seconds))
 
     out = {
         "metric": METRIC,
