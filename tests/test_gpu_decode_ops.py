@@ -327,3 +327,55 @@ def test_decode_layer_chain_graph(qmv, oracle, gpu, hip):
         stream.synchronize()
     for dt in dts.values():
         dt.close()
+
+
+def test_concurrent_streams_share_weights(qmv, gpu, hip):
+    """Four host threads, each with its own stream and buffers, drive the
+    fused SwiGLU, the in-place residual and a 20-position prefill launch on
+    shared device tensors at once; every thread gets the single-threaded
+    bits (each stream has its own workspace: partials, counters, pair
+    counts)."""
+    import threading
+    t4, t6 = B.Q4_K, B.Q6_K
+    dim, hidden = 1536, 4864
+    _, dg = _tensor(qmv, t4, hidden, dim, 140)
+    _, du = _tensor(qmv, t4, hidden, dim, 141)
+    _, dd = _tensor(qmv, t6, dim, hidden, 142)
+    n_threads, positions = 4, 20
+
+    def run(i, stream):
+        x = qmv.synth_normal(dim, seed=150 + i)
+        xp = qmv.synth_normal(positions * dim, seed=160 + i)
+        dx, dxp = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(xp)
+        act = hip.DeviceBuffer(4 * hidden)
+        resid = hip.DeviceBuffer.from_array(qmv.synth_normal(dim, seed=170 + i))
+        pre = hip.DeviceBuffer(4 * positions * hidden)
+        qmv.device_matvec_swiglu(dg, du, dx.ptr, 1, act.ptr, stream.handle)
+        qmv.device_matvec_add_group([dd], act.ptr, 1, [resid.ptr], [dim], [resid.ptr], stream.handle)
+        dg.matvec(dxp.ptr, positions, pre.ptr, stream.handle)
+        stream.synchronize()
+        return (act.to_array(np.float32, (hidden,)), resid.to_array(np.float32, (dim,)),
+                pre.to_array(np.float32, (positions * hidden,)))
+
+    ref = [run(i, hip.Stream()) for i in range(n_threads)]
+    errors = []
+
+    def worker(i):
+        try:
+            s = hip.Stream()
+            for _ in range(8):
+                got = run(i, s)
+                for a, b in zip(got, ref[i]):
+                    if not np.array_equal(_bits(a), _bits(b)):
+                        errors.append(i)
+        except Exception as e:  # pragma: no cover
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(n_threads)]
+    for h in th:
+        h.start()
+    for h in th:
+        h.join()
+    assert not errors, errors
+    for d in (dg, du, dd):
+        d.close()
