@@ -17,6 +17,11 @@
 #define QMV_MFMA_MAX_POSITIONS 32
 /* Tiles (one per wave) per prefill workgroup. */
 #define QMV_PF_TILES 4
+/* Words between the arrival counters of consecutive tiles: one counter per
+ * 128-byte line, so the atomics of different tiles do not queue on a line. */
+#ifndef QMV_COUNTER_STRIDE
+#define QMV_COUNTER_STRIDE 32
+#endif
 
 namespace qmv {
 
@@ -45,7 +50,7 @@ struct MatvecParams {
     int units;          /* K-units per row */
     int units_per_wave; /* contiguous K-units per wave */
     float *partials;
-    unsigned *counters; /* all zero between launches */
+    unsigned *counters; /* all zero between launches; tile t at t * QMV_COUNTER_STRIDE */
     int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
     int positions;    /* positions in this launch (the prefill kernel's position rows past it are padding) */
     /* Fused greedy argmax (single tensor, M = 1; result non-null): tile and
@@ -58,7 +63,8 @@ struct MatvecParams {
     /* Fused SwiGLU (swiglu != 0; jobs 0 = gate and 1 = up, equal rows):
      * job 0's y receives up * silu(gate) and neither projection is stored.
      * Each tile's final values are published to pair_vals[2][tiles][M][64]
-     * and counted in pair_count[tiles] (zero between launches). */
+     * and counted in pair_count[tiles * QMV_COUNTER_STRIDE] (zero between
+     * launches). */
     int swiglu;
     float *pair_vals;
     unsigned *pair_count;

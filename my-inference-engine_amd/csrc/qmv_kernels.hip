@@ -59,6 +59,40 @@ __device__ __forceinline__ float sbyte(uint32_t v, int k)
     return (float)(int)(int8_t)((v >> (8 * k)) & 0xffu);
 }
 
+/* A 4-bit code q held as an integer in bits 0..7 of a 16-bit half reads as
+ * the f16 subnormal q * 2^-24 (16q * 2^-24 for a code in bits 4..7), which
+ * v_fma_mix_f32 widens exactly inside the FMA. fmaf(f16lo(v), x, s) thus adds
+ * q * x * 2^-24 with one rounding: the rounding of fmaf((float)q, x, s') on a
+ * sum scaled by 2^-24, which is exact while sums stay above the fp32
+ * subnormal range (2^-102 unscaled). One instruction per weight instead of a
+ * byte conversion and an FMA. */
+__device__ __forceinline__ float f16lo(uint32_t v)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu));
+}
+__device__ __forceinline__ float f16hi(uint32_t v)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+
+/* Accumulate the 4 low-nibble codes of dword dw (bytes 0..3) against x[0..3]
+ * into l and the 4 high-nibble codes (as 16q) against x[16..19] into h, in
+ * byte order, on sums scaled by 2^-24 (f16lo above). */
+__device__ __forceinline__ void q4_dword_mix(uint32_t dw, const float *x, float &l, float &h)
+{
+    const uint32_t s = dw >> 8;
+    const uint32_t le = dw & 0x000f000fu, lo = s & 0x000f000fu; /* bytes 0,2 | 1,3 */
+    const uint32_t he = dw & 0x00f000f0u, ho = s & 0x00f000f0u;
+    l = fmaf(f16lo(le), x[0], l);
+    l = fmaf(f16lo(lo), x[1], l);
+    l = fmaf(f16hi(le), x[2], l);
+    l = fmaf(f16hi(lo), x[3], l);
+    h = fmaf(f16lo(he), x[16], h);
+    h = fmaf(f16lo(ho), x[17], h);
+    h = fmaf(f16hi(he), x[18], h);
+    h = fmaf(f16hi(ho), x[19], h);
+}
+
 __device__ __forceinline__ float lane_value(float v, int lane)
 {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
@@ -247,26 +281,19 @@ __device__ __forceinline__ float q4k_m1(const Q4KUnit &u, const float *__restric
         const float(&x)[32] = xr[p & 1];
         float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t dw = word(u.p[1 + p], e);
-            const uint32_t lo = codes(dw & 0x0f0f0f0fu), hi = codes(dw & 0xf0f0f0f0u);
-            float &la = (e & 1) ? l1 : l0;
-            float &ha = (e & 1) ? h1 : h0;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                la = fmaf(ubyte(lo, c), x[4 * e + c], la);
-                ha = fmaf(ubyte(hi, c), x[16 + 4 * e + c], ha);
-            }
-        }
+        for (int e = 0; e < 4; ++e)
+            q4_dword_mix(word(u.p[1 + p], e), x + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
         slo[g] += l0 + l1;
         shi[g] += h0 + h1;
     }
+    /* slo / shi hold sums scaled by 2^-24 (q4_dword_mix): the scales carry
+     * 2^24 (low codes q) and 2^24 / 16 (high codes 16q), exact powers of 2. */
     const Q4KScales s = q4k_scales(u.p[0]);
     float acc = 0.0f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        acc = fmaf(s.a[2 * g], slo[g], acc);
-        acc = fmaf(s.a[2 * g + 1], shi[g], acc);
+        acc = fmaf(s.a[2 * g] * 16777216.0f, slo[g], acc);
+        acc = fmaf(s.a[2 * g + 1] * 16777216.0f, shi[g], acc);
         acc = fmaf(-s.m[2 * g], lane_value(xs, 16 * g), acc);
         acc = fmaf(-s.m[2 * g + 1], lane_value(xs, 16 * g + 8), acc);
     }
@@ -857,7 +884,7 @@ __device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork 
     for (int m = 0; m < M; ++m) store_partial(mine + m * 64, v[m]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(p.pair_count + w.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) prev = __hip_atomic_fetch_add(p.pair_count + w.tile * QMV_COUNTER_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
     if (prev == 0u) return;
     asm volatile("" ::: "memory");
@@ -869,7 +896,7 @@ __device__ __forceinline__ void swiglu_pair(const MatvecParams &p, const WgWork 
         const float u = w.job == 0 ? o : v[m];
         if (valid && m < npos) out.y[(size_t)m * out.ldy + row] = swiglu_value(g, u);
     }
-    if (lane == 0) __hip_atomic_store(p.pair_count + w.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(p.pair_count + w.tile * QMV_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* A tile's final row values v[m] (lane = row within the tile): add the
@@ -926,7 +953,7 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
 
     if (job.splits > 1) {
         float *part = p.partials + job.partial_offset + ((size_t)w.tile * job.splits) * M * 64;
-        unsigned *count = p.counters + job.counter_offset + w.tile;
+        unsigned *count = p.counters + job.counter_offset + w.tile * QMV_COUNTER_STRIDE;
 #pragma unroll
         for (int m = 0; m < M; ++m) store_partial(part + ((size_t)w.split * M + m) * 64 + lane, sum[m]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1566,7 +1593,7 @@ __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned prev = 0;
         if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.pair_count + w.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            prev = __hip_atomic_fetch_add(p.pair_count + w.tile * QMV_COUNTER_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
         if (prev == 0u) return;
         asm volatile("" ::: "memory");
@@ -1584,7 +1611,7 @@ __device__ __forceinline__ void pf_emit(const MatvecParams &p, const WgWork &w, 
                 if (valid) out.y[(size_t)(m0 + i) * out.ldy + row] = swiglu_value(g, u);
             }
         }
-        if (lane == 0) __hip_atomic_store(p.pair_count + w.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(p.pair_count + w.tile * QMV_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     if (valid)
@@ -1598,7 +1625,7 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
     const int S = job.splits;
     if (S > 1) {
         float *part = p.partials + job.partial_offset + ((size_t)w.tile * S) * MP * 64 + lane;
-        unsigned *count = p.counters + job.counter_offset + w.tile;
+        unsigned *count = p.counters + job.counter_offset + w.tile * QMV_COUNTER_STRIDE;
         for (int m = 0; m < npos; ++m) store_partial(part + ((size_t)w.split * MP + m) * 64, val[m * 64 + lane]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned prev = 0;

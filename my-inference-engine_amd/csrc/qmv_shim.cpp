@@ -543,7 +543,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         }
         if (plan.splits > 1) {
             partials += (size_t)ts[i]->tiles * plan.splits * mt * 64;
-            counters += (size_t)ts[i]->tiles;
+            counters += (size_t)ts[i]->tiles * QMV_COUNTER_STRIDE;
         }
         wg += (long long)(prefill ? (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES : ts[i]->tiles) * plan.splits;
     }
@@ -556,7 +556,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
             return 0;
         }
         partials += (size_t)2 * t0->tiles * mt * 64;
-        counters += (size_t)t0->tiles;
+        counters += (size_t)t0->tiles * QMV_COUNTER_STRIDE;
         p.swiglu = 1;
     }
     if (wg > INT_MAX || partials > (size_t)INT_MAX || counters > (size_t)INT_MAX) {
