@@ -75,6 +75,19 @@ __device__ __forceinline__ float f16hi(uint32_t v)
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
 }
 
+/* Accumulate the 4 byte codes (each < 1024) of dword q against x[0..3], in
+ * byte order, on a sum scaled by 2^-24 (f16lo above). */
+__device__ __forceinline__ float byte_codes_mix(uint32_t q, const float *x, float a)
+{
+    /* bytes 0,2 | bytes 1,3 (v_perm_b32 selector 0x0c = zero byte) */
+    const uint32_t ev = q & 0x00ff00ffu, od = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);
+    a = fmaf(f16lo(ev), x[0], a);
+    a = fmaf(f16lo(od), x[1], a);
+    a = fmaf(f16hi(ev), x[2], a);
+    a = fmaf(f16hi(od), x[3], a);
+    return a;
+}
+
 /* Accumulate the 4 low-nibble codes of dword dw (bytes 0..3) against x[0..3]
  * into l and the 4 high-nibble codes (as 16q) against x[16..19] into h, in
  * byte order, on sums scaled by 2^-24 (f16lo above). */
@@ -388,22 +401,21 @@ __device__ __forceinline__ float q6k_m1(const Q6KUnit &u, const float *__restric
             q1 = codes(q1);
             float &a0 = (e & 1) ? c01 : c00;
             float &a1 = (e & 1) ? c11 : c10;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                a0 = fmaf(ubyte(q0, c), x[4 * e + c], a0);
-                a1 = fmaf(ubyte(q1, c), x[16 + 4 * e + c], a1);
-            }
+            a0 = byte_codes_mix(q0, x + 4 * e, a0);
+            a1 = byte_codes_mix(q1, x + 16 + 4 * e, a1);
         }
         const int j0 = 8 * g + 4 * rp + oh; /* r = 2rp: j = 8g + 2r + oh */
         sg[j0] += c00 + c01;
         sg[j0 + 2] += c10 + c11;
     }
+    /* sg holds sums of q * x scaled by 2^-24 (byte_codes_mix); the offset
+     * term 32 * sum(x) is scaled to match, exactly. */
     float dsc[16];
     q6k_dscales(u, dsc);
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) /* scale group j covers x[16j .. 16j+15] */
-        acc = fmaf(dsc[j], fmaf(-32.0f, lane_value(xs, 4 * j), sg[j]), acc);
+        acc = fmaf(dsc[j] * 16777216.0f, fmaf(-1.9073486328125e-6f, lane_value(xs, 4 * j), sg[j]), acc);
     return acc;
 }
 
