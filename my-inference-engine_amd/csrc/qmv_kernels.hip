@@ -1054,14 +1054,46 @@ typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 /* A per-lane pointer that cannot be used before `dep` exists: ties the
  * activation loads of a sub-block to the accumulators of an earlier one, so
  * the loads are not all hoisted to the top of the unrolled unit. */
-__device__ __forceinline__ const float *ptr_after(const float *p, float dep)
+/* Global-memory (address space 1) views. The ordering asm below hides a
+ * pointer's origin, and a generic pointer would then load with flat
+ * instructions, which also count against lgkmcnt (so scalar-load waits would
+ * wait for them); through these types the loads stay global_load. */
+typedef const float __attribute__((address_space(1))) gf32;
+typedef const uint8_t __attribute__((address_space(1))) gu8;
+typedef const uint32_t __attribute__((address_space(1))) gu32;
+typedef const unsigned short __attribute__((address_space(1))) gu16;
+typedef unsigned int u32v4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32v2 __attribute__((ext_vector_type(2)));
+typedef const u32v4 __attribute__((address_space(1))) gv4;
+typedef const u32v2 __attribute__((address_space(1))) gv2;
+
+__device__ __forceinline__ uint4 gload16(gu8 *p)
 {
-    asm("" : "+v"(p) : "v"(dep));
-    return p;
+    const u32v4 v = *(gv4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 gload8(gu8 *p)
+{
+    const u32v2 v = *(gv2 *)p;
+    return make_uint2(v.x, v.y);
 }
 
-template <int KL>
-__device__ __forceinline__ void load_x(float (&v)[KL], const float *p)
+__device__ __forceinline__ gf32 *ptr_after(const float *p, float dep)
+{
+    gf32 *g = (gf32 *)p;
+    asm("" : "+v"(g) : "v"(dep));
+    return g;
+}
+
+__device__ __forceinline__ gu8 *bytes_after(const uint8_t *p, float dep)
+{
+    gu8 *g = (gu8 *)p;
+    asm("" : "+v"(g) : "v"(dep));
+    return g;
+}
+
+template <int KL, typename P>
+__device__ __forceinline__ void load_x(float (&v)[KL], P *p)
 {
 #pragma unroll
     for (int j = 0; j < KL; ++j) v[j] = p[j];
@@ -1105,7 +1137,7 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
                            (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
     float xv[2][8];
-    load_x<8>(xv[0], xp);
+    load_x<8>(xv[0], (gf32 *)xp);
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         const int c = sb >> 1;
@@ -1114,9 +1146,9 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
          * group's codes, load while this sub-block runs. */
         if (sb + 1 < 8) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
         if (!high && c + 1 < 4) {
-            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[1][0]);
+            gu8 *nq = bytes_after(qsp + (c + 1) * 2048, acc[1][0]);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
+            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
         }
         bf16x8_t a0, a1, a2;
         x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
@@ -1197,7 +1229,7 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
     }
     float xv[2][4];
-    load_x<4>(xv[0], xp);
+    load_x<4>(xv[0], (gf32 *)xp);
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
         const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
@@ -1209,12 +1241,12 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         }
         if (r == 0 && pr + 1 < 4) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
-            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[1][0]);
+            gu8 *np = bytes_after(wp, acc[1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                w[(pr + 1) & 1][g][0] = *(const uint32_t *)(np + (4 * Gn + hn) * 1024 + g * 256);
-                w[(pr + 1) & 1][g][1] = *(const uint32_t *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
-                w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][0] = *(gu32 *)(np + (4 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][1] = *(gu32 *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][2] = *(gu32 *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
             }
         }
         bf16x4_t a0, a1, a2;
@@ -1395,16 +1427,16 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
         const int c = sb >> 1;
         const bool high = sb & 1;
         if (!high && c + 1 < 4) {
-            const uint8_t *nq = (const uint8_t *)ptr_after((const float *)(qsp + (c + 1) * 2048), acc[0][1][0]);
+            gu8 *nq = bytes_after(qsp + (c + 1) * 2048, acc[0][1][0]);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = *(const uint2 *)(nq + g * 256);
+            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
         }
         if (sb == QMV_PF_NEXT_SB) {
-            const uint8_t *np = (const uint8_t *)ptr_after((const float *)next, acc[0][2][0]);
+            gu8 *np = bytes_after(next, acc[0][2][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                hn[g] = ld16(np + n * 16 + g * 256);
-                qn[g] = *(const uint2 *)(np + qoff + g * 256);
+                hn[g] = gload16(np + n * 16 + g * 256);
+                qn[g] = gload8(np + qoff + g * 256);
             }
         }
         const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
@@ -1501,23 +1533,23 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
         const int j = 8 * G + 2 * r + (pr & 1);
         if (r == 0 && pr + 1 < 4) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
-            const uint8_t *np = (const uint8_t *)ptr_after((const float *)wp, acc[0][1][0]);
+            gu8 *np = bytes_after(wp, acc[0][1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                w[(pr + 1) & 1][g][0] = *(const uint32_t *)(np + (4 * Gn + hn) * 1024 + g * 256);
-                w[(pr + 1) & 1][g][1] = *(const uint32_t *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
-                w[(pr + 1) & 1][g][2] = *(const uint32_t *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][0] = *(gu32 *)(np + (4 * Gn + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][1] = *(gu32 *)(np + (4 * Gn + 2 + hn) * 1024 + g * 256);
+                w[(pr + 1) & 1][g][2] = *(gu32 *)(np + (8 + 2 * Gn + hn) * 1024 + g * 256);
             }
         }
         if (t == QMV_PF_NEXT_T) {
-            const uint8_t *np = (const uint8_t *)ptr_after((const float *)next, acc[0][2][0]);
+            gu8 *np = bytes_after(next, acc[0][2][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                scn[g] = ld16(np + 12 * 1024 + (16 * g + n) * 16);
-                dgn[g] = *(const unsigned short *)(np + 13312 + (16 * g + n) * 2);
-                wn[g][0] = *(const uint32_t *)(np + woff + 0 * 1024 + g * 256);
-                wn[g][1] = *(const uint32_t *)(np + woff + 2 * 1024 + g * 256);
-                wn[g][2] = *(const uint32_t *)(np + woff + 8 * 1024 + g * 256);
+                scn[g] = gload16(np + 12 * 1024 + (16 * g + n) * 16);
+                dgn[g] = *(gu16 *)(np + 13312 + (16 * g + n) * 2);
+                wn[g][0] = *(gu32 *)(np + woff + 0 * 1024 + g * 256);
+                wn[g][1] = *(gu32 *)(np + woff + 2 * 1024 + g * 256);
+                wn[g][2] = *(gu32 *)(np + woff + 8 * 1024 + g * 256);
             }
         }
         bf16x4_t b[4];
