@@ -1116,6 +1116,25 @@ __device__ __forceinline__ void x_limbs(const float (&xv)[KL], bool valid, V &h,
     }
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+/* Eight Q4_K codes, bytes 0..3 of lo then of hi (low nibbles, or the high
+ * nibbles shifted down), as an exact bf16 MFMA operand. A code q in the low
+ * bits of a byte is the FP8 E4M3 pattern of q * 2^-9 (subnormals for 0..7,
+ * the first normal binade for 8..15), which v_cvt_scalef32_pk_bf16_fp8
+ * converts with the scale 2^9 to bf16(q) exactly, two codes per
+ * instruction. */
+__device__ __forceinline__ bf16x8_t q4_codes_bf16(uint32_t lo, uint32_t hi, bool high)
+{
+    lo = (high ? lo >> 4 : lo) & 0x0f0f0f0fu;
+    hi = (high ? hi >> 4 : hi) & 0x0f0f0f0fu;
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true);
+    return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 template <int M>
 __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
                                               f32x4_t (&acc)[4])
@@ -1152,20 +1171,10 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
         }
         bf16x8_t a0, a1, a2;
         x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
-        /* High nibbles are used in place as 16 * q; 1/16 is folded into the
-         * sub-block scale (exact). */
-        const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
         bf16x8_t b[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t lo = codes(after(q[c & 1][g].x, acc[g][0]) & mask);
-            const uint32_t hi = codes(after(q[c & 1][g].y, acc[g][0]) & mask);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                b[g][j] = (__bf16)ubyte(lo, j);
-                b[g][4 + j] = (__bf16)ubyte(hi, j);
-            }
-        }
+        for (int g = 0; g < 4; ++g)
+            b[g] = q4_codes_bf16(after(q[c & 1][g].x, acc[g][0]), after(q[c & 1][g].y, acc[g][0]), high);
         f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1192,8 +1201,7 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
                 scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
                 mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
             }
-            float sa = dd * ubyte(scw, sb & 3);
-            if (high) sa *= 0.0625f;
+            const float sa = dd * ubyte(scw, sb & 3);
             const float sm = dmin * ubyte(mw, sb & 3);
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[g][j] = fmaf(sa, d[g][j], fmaf(-sm, xs[j], acc[g][j]));
@@ -1439,18 +1447,10 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
                 qn[g] = gload8(np + qoff + g * 256);
             }
         }
-        const uint32_t mask = high ? 0xf0f0f0f0u : 0x0f0f0f0fu;
         bf16x8_t b[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t lo = codes(after(q[c & 1][g].x, acc[0][g][0]) & mask);
-            const uint32_t hi = codes(after(q[c & 1][g].y, acc[0][g][0]) & mask);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                b[g][j] = (__bf16)ubyte(lo, j);
-                b[g][4 + j] = (__bf16)ubyte(hi, j);
-            }
-        }
+        for (int g = 0; g < 4; ++g)
+            b[g] = q4_codes_bf16(after(q[c & 1][g].x, acc[0][g][0]), after(q[c & 1][g].y, acc[0][g][0]), high);
         float sa[4], sm[4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
@@ -1487,7 +1487,6 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
                         mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
                     }
                     sa[g] = dd * ubyte(scw, sb & 3);
-                    if (high) sa[g] *= 0.0625f;
                     sm[g] = dmin * ubyte(mw, sb & 3);
                 }
             }
