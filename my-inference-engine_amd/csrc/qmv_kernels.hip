@@ -1135,13 +1135,33 @@ __device__ __forceinline__ bf16x8_t q4_codes_bf16(uint32_t lo, uint32_t hi, bool
     return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+/* Four Q6_K codes of one sub-block (4(r>>1)-shifted nibbles of the ql word
+ * lw, 2r-shifted 2-bit fields of the qh word hw) as two exact bf16 operands
+ * whose sum is q - 32: lo = the low nibble (FP8 E4M3 pattern of lo * 2^-9,
+ * scale 2^9) and hi = 16 * (h - 2), from the sign-magnitude E4M3 patterns of
+ * h - 2 = -2..1 picked by v_perm_b32 from the table 0x82, 0x81, 0x00, 0x01
+ * (scale 2^13). The matrix core adds both products into one accumulator. */
+__device__ __forceinline__ void q6_codes_bf16(uint32_t lw, uint32_t hw, int r, bf16x4_t &lo, bf16x4_t &hi)
+{
+    const uint32_t l = (lw >> (4 * (r >> 1))) & 0x0f0f0f0fu;
+    const uint32_t h = __builtin_amdgcn_perm(0u, 0x01008182u, (hw >> (2 * r)) & 0x03030303u);
+    const bf16x2_t l0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l, 512.0f, false);
+    const bf16x2_t l1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l, 512.0f, true);
+    const bf16x2_t h0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h, 8192.0f, false);
+    const bf16x2_t h1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h, 8192.0f, true);
+    lo = bf16x4_t{l0[0], l0[1], l1[0], l1[1]};
+    hi = bf16x4_t{h0[0], h0[1], h1[0], h1[1]};
+}
+
 template <int M>
 __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
                                               f32x4_t (&acc)[4])
 {
     const int kc = lane >> 4, n = lane & 15;
     const bool valid = n < M;
-    /* Lanes past the batch read position 0 (in bounds) and use zeros. */
+    /* Lanes past the batch read position 0 (in bounds): their products land
+     * in accumulator rows >= M, which the kernel never stores, so their
+     * limbs need not be zeroed. */
     const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
     /* This lane's bytes of row 16g + n: header, and the 8 qs bytes of its
      * k-chunk in 64-weight group c (plane 1 + 2c + kc/2). */
@@ -1170,7 +1190,7 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
             for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
         }
         bf16x8_t a0, a1, a2;
-        x_limbs<8>(xv[sb & 1], valid, a0, a1, a2);
+        x_limbs<8>(xv[sb & 1], true, a0, a1, a2);
         bf16x8_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
@@ -1219,6 +1239,7 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
 {
     const int kc = lane >> 4, n = lane & 15;
     const bool valid = n < M;
+    /* Lanes past the batch read position 0; their rows are never stored. */
     const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 4 * kc;
     const uint8_t *wp = slab + n * 16 + 4 * kc; /* this lane's dword of row 16g + n in a plane */
     uint4 sc[4];
@@ -1258,25 +1279,29 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
             }
         }
         bf16x4_t a0, a1, a2;
-        x_limbs<4>(xv[t & 1], valid, a0, a1, a2);
-        bf16x4_t b[4];
+        x_limbs<4>(xv[t & 1], true, a0, a1, a2);
+        bf16x4_t bl[4], bh[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[g][0]);
-            const uint32_t hw = after(w[pr & 1][g][2], acc[g][0]);
-            const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
-        }
+        for (int g = 0; g < 4; ++g)
+            q6_codes_bf16(after(w[pr & 1][g][r & 1], acc[g][0]), after(w[pr & 1][g][2], acc[g][0]), r, bl[g], bh[g]);
         f32x4_t d[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, bl[g], d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, bh[g], d[g], 0, 0, 0);
+        }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, bl[g], d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, bh[g], d[g], 0, 0, 0);
+        }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, bl[g], d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, bh[g], d[g], 0, 0, 0);
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const float s = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
@@ -1551,6 +1576,11 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
                 wn[g][2] = *(gu32 *)(np + woff + 8 * 1024 + g * 256);
             }
         }
+        /* One combined operand per code (q - 32, exact in bf16), converted
+         * once for every position block. The two-operand form of the M <= 8
+         * kernel (q6_codes_bf16) would double the MFMAs of each block, and
+         * using it for one block only would make a position's rounding depend
+         * on the number of positions in its launch. */
         bf16x4_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -1558,7 +1588,7 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
             const uint32_t hw = after(w[pr & 1][g][2], acc[0][g][0]);
             const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f);
+            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
         }
         float s[4];
 #pragma unroll
