@@ -257,6 +257,26 @@ def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
     matvec_parity(qmv, oracle, t, rows, cols, seed=rows + cols, what="odd shape")
 
 
+@pytest.mark.parametrize("t", B.ALL_TYPES)
+@pytest.mark.parametrize("batch", [1, 8, 20])
+@pytest.mark.parametrize("scale", ["1e-28", "1e28", "mixed"])
+def test_activation_dynamic_range(qmv, oracle, gpu, t, batch, scale):
+    """Activations far from N(0,1) stay within the row bar on every kernel:
+    M = 1 on the VALU (Q4_K/Q6_K codes on v_fma_mix_f32, whose sums run scaled
+    by 2^-24), M = 8 on the matrix cores (exact bf16 limbs), 20 positions in
+    the prefill kernel (Q8_0/Q5_0: passes of 8 on the VALU). The whole vector
+    at 1e-28 or 1e28, or magnitudes from 1e-20 to 1e20 element by element."""
+    cols = 4 * 256
+    rng = np.random.default_rng(batch * 7 + len(scale))
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    if scale == "mixed":
+        x *= (10.0 ** rng.integers(-20, 21, size=x.shape)).astype(np.float32)
+    else:
+        x *= np.float32(float(scale))
+    assert np.isfinite(x).all()
+    matvec_parity(qmv, oracle, t, 130, cols, batch=batch, seed=batch + 90, x=x, what=f"range {scale}")
+
+
 # Launch plans: (target_waves, units_per_wave, waves_per_group,
 # mfma_min_batch). The default gives every wave one unit (the single-unit
 # kernel variant) and runs Q4_K batches of 7 or more and Q6_K batches of 8 on
