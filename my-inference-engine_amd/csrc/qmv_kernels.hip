@@ -1039,14 +1039,17 @@ matvec_kernel(MatvecParams p)
  * 8 positions.
  *
  * MFMA operand roles (lane l, kc = l / 16, n = l % 16): A = limbs, row i =
- * position (rows >= M are zero), lane l supplies A[n][kc*KL + j]; B = weight
+ * position (rows >= M repeat position 0 and are never stored), lane l
+ * supplies A[n][kc*KL + j]; B = weight
  * codes, column = weight row 16g + n of row group g, lane l supplies
  * B[kc*KL + j][n]; D[i][n] lands in lane n + 16*(i/4), element i % 4. So a
  * lane's accumulator holds positions 4*kc..4*kc+3 of one weight row, and the
  * per-row scales it applies are that row's own. KL = 8 (16x16x32 MFMA, Q4_K
  * sub-blocks of 32) or 4 (16x16x16, Q6_K sub-blocks of 16). Per sub-block the
  * MFMAs of the four row groups are issued limb by limb, so four (five with
- * Q4_K's sum(x)) independent accumulations keep the matrix pipe busy. */
+ * Q4_K's sum(x)) independent accumulations keep the matrix pipe busy. The
+ * codes reach bf16 through the FP8 converter (q4_codes_bf16, q6_codes_bf16
+ * below). */
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
