@@ -427,13 +427,16 @@ struct Plan {
 };
 
 /* Default: one K-unit per wave, four waves per workgroup (one per SIMD), or
- * eight for long rows (>= 32 K-units), where fewer splits per tile means
- * fewer partials for the last split to add. Many short workgroups keep every
- * CU streaming until the end and let the dispatcher balance the load; on
- * MI355X this beat longer waves and stream-K partitions at every decode shape
- * measured. With target_waves set, units per wave grow instead until about
- * that many waves cover the launch. */
-Plan plan_for(long long total_tiles, int units)
+ * `long_waves` for long rows (>= 32 K-units), where fewer splits per tile
+ * means fewer partials for the last split to add: 6 at M = 1 (down 3584 x
+ * 18944 Q6_K: 14.4 us against 15.8 at 8 and 15.1 at 4, whose 19 splits need
+ * two rounds of partial loads), 8 for batches (the matrix-core down at M = 8
+ * is 1-2% slower at 6). Many short workgroups keep every CU streaming until
+ * the end and let the dispatcher balance the load; on MI355X this beat longer
+ * waves and stream-K partitions at every decode shape measured. With
+ * target_waves set, units per wave grow instead until about that many waves
+ * cover the launch. */
+Plan plan_for(long long total_tiles, int units, int long_waves)
 {
     const int target = g_target_waves.load();
     const int force_u = g_force_u.load();
@@ -445,7 +448,7 @@ Plan plan_for(long long total_tiles, int units)
     }
     if (force_u > 0) U = force_u;
     if (U > units) U = units;
-    int W = force_w > 0 ? force_w : target > 0 || units >= 32 ? QMV_MAX_WAVES : 4;
+    int W = force_w > 0 ? force_w : target > 0 ? QMV_MAX_WAVES : units >= 32 ? long_waves : 4;
     const int need = (units + U - 1) / U;
     if (W > need) W = need;
     int S = (units + W * U - 1) / (W * U);
@@ -512,7 +515,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         total_tiles += ts[i]->tiles;
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
-    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units);
+    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units, batch == 1 ? 6 : QMV_MAX_WAVES);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
