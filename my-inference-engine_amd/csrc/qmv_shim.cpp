@@ -426,13 +426,13 @@ struct Plan {
     int units_per_wave, waves, splits, units_per_split;
 };
 
-/* Default: one K-unit per wave, four waves per workgroup (one per SIMD), or
- * `long_waves` for long rows (>= 32 K-units), where fewer splits per tile
- * means fewer partials for the last split to add: 6 at M = 1 (down 3584 x
- * 18944 Q6_K: 14.4 us against 15.8 at 8 and 15.1 at 4, whose 19 splits need
- * two rounds of partial loads), 8 for batches (the matrix-core down at M = 8
- * is 1-2% slower at 6). Many short workgroups keep every CU streaming until
- * the end and let the dispatcher balance the load; on MI355X this beat longer
+/* Default: one K-unit per wave and four waves per workgroup (one per SIMD);
+ * for long rows (>= 32 K-units) at M = 1, `long_waves` = 6: down 3584 x
+ * 18944 Q6_K takes 14.4 us against 15.8 at 8 and 15.1 at 4, whose 19 splits
+ * need two rounds of partial loads. Batches keep 4 for long rows too (down at
+ * M = 8: 42.2 us against 45 at 8; 1536 x 8960 Q4_K at M = 2 and 4: 9-10%
+ * faster than at 8). Many short workgroups keep every CU streaming until the
+ * end and let the dispatcher balance the load; on MI355X this beat longer
  * waves and stream-K partitions at every decode shape measured. With
  * target_waves set, units per wave grow instead until about that many waves
  * cover the launch. */
@@ -515,7 +515,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         total_tiles += ts[i]->tiles;
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
-    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units, batch == 1 ? 6 : QMV_MAX_WAVES);
+    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units, batch == 1 ? 6 : 4);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
