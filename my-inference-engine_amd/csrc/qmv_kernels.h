@@ -68,6 +68,13 @@ struct MatvecParams {
     int swiglu;
     float *pair_vals;
     unsigned *pair_count;
+    /* Paired SwiGLU (M = 1, pair_waves > 0; swiglu then 0): a workgroup runs
+     * the same tile and K-range of job 0 (gate) in waves [0, pair_waves) and
+     * of job 1 (up) in waves [pair_waves, 2 pair_waves), and its finisher
+     * writes up * silu(gate) to job 0's y. A split publishes both sums
+     * (partials [tiles][splits][2][64] at job 0's offsets), so no second
+     * count per tile pair is needed. */
+    int pair_waves;
 };
 
 /* Workspace of a fused argmax over `tiles` tiles (groups of 64 tiles). */

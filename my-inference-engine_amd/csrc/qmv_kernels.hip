@@ -862,6 +862,18 @@ struct WgWork {
 __device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave)
 {
     WgWork w;
+    if (p.pair_waves > 0) { /* paired SwiGLU: gate waves, then up waves */
+        const int half = wave >= p.pair_waves ? 1 : 0;
+        const MatvecJob &job = p.job[0];
+        w.job = half;
+        w.tile = blockIdx.x / job.splits;
+        w.split = blockIdx.x - w.tile * job.splits;
+        const int split_begin = w.split * job.units_per_split;
+        const int split_end = min(split_begin + job.units_per_split, p.units);
+        w.u_begin = split_begin + (wave - half * p.pair_waves) * p.units_per_wave;
+        w.u_end = min(w.u_begin + p.units_per_wave, split_end);
+        return w;
+    }
     int j = 0;
     while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
     const MatvecJob &job = p.job[j];
@@ -950,10 +962,53 @@ __device__ __forceinline__ void emit_tile(const MatvecParams &p, const WgWork &w
  * wait for the partial stores to complete orders them before the arrival
  * count. The last split resets the counter, so the workspace needs no
  * clearing between launches. */
+/* Paired SwiGLU finish (M = 1): gate and up sums of the tile, each over its
+ * waves in wave order and its splits in split order (the order of the two
+ * separate launches), then up * silu(gate) into job 0's y. */
+__device__ __forceinline__ void finish_paired(const MatvecParams &p, const WgWork &w, int lane,
+                                              const float (*red)[1][64])
+{
+    const int W = p.pair_waves;
+    float g = red[0][0][lane], u = red[W][0][lane];
+    for (int v = 1; v < W; ++v) {
+        g += red[v][0][lane];
+        u += red[W + v][0][lane];
+    }
+    const MatvecJob &gj = p.job[0], &uj = p.job[1];
+    const int S = gj.splits;
+    if (S > 1) {
+        float *part = p.partials + gj.partial_offset + (size_t)w.tile * S * 128 + lane;
+        unsigned *count = p.counters + gj.counter_offset + w.tile * QMV_COUNTER_STRIDE;
+        store_partial(part + (size_t)w.split * 128, g);
+        store_partial(part + (size_t)w.split * 128 + 64, u);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
+        if (prev != (unsigned)S - 1u) return;
+        asm volatile("" ::: "memory");
+        g = sum_partials(part, 128, S);
+        u = sum_partials(part + 64, 128, S);
+        if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int row = w.tile * 64 + lane;
+    if (row < gj.rows) {
+        if (gj.add != nullptr) g += gj.add[row];
+        if (uj.add != nullptr) u += uj.add[row];
+        gj.y[row] = swiglu_value(g, u);
+    }
+}
+
 template <int M>
 __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork &w, int nwaves, int lane,
                                             const float (*red)[M][64], int npos = M)
 {
+    if constexpr (M == 1) {
+        if (p.pair_waves > 0) {
+            finish_paired(p, w, lane, red);
+            return;
+        }
+    }
     const MatvecJob &job = p.job[w.job];
     float sum[M];
 #pragma unroll

@@ -414,6 +414,9 @@ std::atomic<int> g_force_w{env_int("QMV_WAVES_PER_GROUP", 0)};
  * MI355X at Qwen2.5-7B layer shapes: 7 for Q4_K, 8 for Q6_K (its code
  * assembly costs more VALU per weight on the matrix-core path). */
 std::atomic<int> g_mfma_min_batch{env_int("QMV_MFMA_MIN_BATCH", 0)};
+/* QMV_PAIRED_SWIGLU=0 runs the fused SwiGLU with the tile-pair count instead
+ * of paired workgroups (for comparison). */
+std::atomic<int> g_paired_swiglu{env_int("QMV_PAIRED_SWIGLU", 1)};
 
 bool use_matrix_cores(int fmt, int batch)
 {
@@ -526,6 +529,12 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     p.units = t0->units;
     p.units_per_wave = plan.units_per_wave;
     p.positions = batch;
+    /* Fused SwiGLU at M = 1 with one unit per wave: one workgroup per
+     * (tile, split) of both projections (finish_paired), when the two halves
+     * fit a workgroup. */
+    const bool paired = epi.swiglu && count == 2 && batch == 1 && !prefill && !mfma &&
+                        plan.units_per_wave == 1 && 2 * plan.waves <= QMV_MAX_WAVES &&
+                        ts[0]->rows == ts[1]->rows && g_paired_swiglu.load() != 0;
     size_t partials = 0, counters = 0;
     long long wg = 0;
     for (int i = 0; i < count; ++i) {
@@ -544,16 +553,27 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
             j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
             j.ldadd = epi.ldadd[i];
         }
+        if (paired) {
+            if (i == 0) { /* two sums per split, one count per tile, in job 0's regions */
+                if (plan.splits > 1) {
+                    partials += (size_t)ts[0]->tiles * plan.splits * 2 * 64;
+                    counters += (size_t)ts[0]->tiles * QMV_COUNTER_STRIDE;
+                }
+                wg += (long long)ts[0]->tiles * plan.splits;
+            }
+            continue;
+        }
         if (plan.splits > 1) {
             partials += (size_t)ts[i]->tiles * plan.splits * mt * 64;
             counters += (size_t)ts[i]->tiles * QMV_COUNTER_STRIDE;
         }
         wg += (long long)(prefill ? (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES : ts[i]->tiles) * plan.splits;
     }
-    /* Fused SwiGLU: both projections' final tiles, then one count per tile
-     * pair, after the split-K partials and counters. */
+    if (paired) p.pair_waves = plan.waves;
+    /* Fused SwiGLU otherwise: both projections' final tiles, then one count
+     * per tile pair, after the split-K partials and counters. */
     const size_t pair_vals = partials, pair_count = counters;
-    if (epi.swiglu) {
+    if (epi.swiglu && !paired) {
         if (count != 2 || ts[0]->rows != ts[1]->rows) {
             set_error("fused SwiGLU takes two tensors (gate, up) with equal rows");
             return 0;
@@ -571,7 +591,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (!workspace_reserve(ws, stream, partials, counters)) return 0;
     p.partials = ws.partials;
     p.counters = ws.counters;
-    if (epi.swiglu) {
+    if (epi.swiglu && !paired) {
         p.pair_vals = ws.partials + pair_vals;
         p.pair_count = ws.counters + pair_count;
     }
@@ -589,7 +609,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (prefill)
         HIP_TRY(qmv::launch_prefill(t0->geo.format, p, mt, (int)wg, stream));
     else
-        HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, plan.waves, stream));
+        HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, paired ? 2 * plan.waves : plan.waves, stream));
     return 1;
 }
 

@@ -160,7 +160,8 @@ def _ulp_close(got, ref):
 
 @pytest.mark.parametrize("t,rows,cols,batch", [
     (B.Q4_K, 18944, 3584, 1), (B.Q4_K, 18944, 3584, 8), (B.Q4_K, 8960, 1536, 3),
-    (B.Q6_K, 1000, 896 * 4, 2), (B.Q8_0, 4864, 896, 1), (B.Q5_0, 130, 1536, 5), (B.Q4_K, 65, 256, 7)])
+    (B.Q6_K, 1000, 896 * 4, 2), (B.Q8_0, 4864, 896, 1), (B.Q5_0, 130, 1536, 5), (B.Q4_K, 65, 256, 7),
+    (B.Q6_K, 1000, 896 * 4, 1), (B.Q5_0, 130, 1536, 1), (B.Q4_K, 65, 256, 1), (B.Q4_K, 4864, 18944, 1)])
 def test_swiglu_fused_matches_oracle(qmv, oracle, gpu, hip, t, rows, cols, batch):
     log(f"fused SwiGLU type {t} {rows}x{cols} M={batch}")
     raw_g, dg = _tensor(qmv, t, rows, cols, 100)
