@@ -859,7 +859,7 @@ struct WgWork {
     int job, tile, split, u_begin, u_end;
 };
 
-__device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave)
+__device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave, int items)
 {
     WgWork w;
     if (p.pair_waves > 0) { /* paired SwiGLU: gate waves, then up waves */
@@ -882,7 +882,7 @@ __device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave)
     w.tile = local / job.splits;
     w.split = local - w.tile * job.splits;
     const int split_begin = w.split * job.units_per_split;
-    const int split_end = min(split_begin + job.units_per_split, p.units);
+    const int split_end = min(split_begin + job.units_per_split, items);
     w.u_begin = split_begin + wave * p.units_per_wave;
     w.u_end = min(w.u_begin + p.units_per_wave, split_end);
     return w;
@@ -1050,7 +1050,7 @@ matvec_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgWork w = locate(p, wave);
+    const WgWork w = locate(p, wave, p.units);
     const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
     float acc[M];
 #pragma unroll
@@ -1157,24 +1157,35 @@ __device__ __forceinline__ void load_x(float (&v)[KL], P *p)
     for (int j = 0; j < KL; ++j) v[j] = p[j];
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 /* The three bf16 limbs of KL activations of one position (zero when the lane
- * carries no position). */
+ * carries no position), two activations at a time: one round-to-nearest-even
+ * conversion per limb pair (v_cvt_pk_bf16_f32), and the pair's bf16 values
+ * widened back to fp32 by a shift and a mask of the packed bits. */
 template <int KL, typename V>
 __device__ __forceinline__ void x_limbs(const float (&xv)[KL], bool valid, V &h, V &m, V &l)
 {
+    static_assert(KL % 2 == 0, "pairs of activations");
 #pragma unroll
-    for (int j = 0; j < KL; ++j) {
-        const float v = valid ? xv[j] : 0.0f;
-        const __bf16 vh = (__bf16)v;
-        const float r = v - (float)vh;
-        const __bf16 vm = (__bf16)r;
-        h[j] = vh;
-        m[j] = vm;
-        l[j] = (__bf16)(r - (float)vm);
+    for (int j = 0; j < KL; j += 2) {
+        const float v0 = valid ? xv[j] : 0.0f, v1 = valid ? xv[j + 1] : 0.0f;
+        const bf16x2_t hp = __builtin_convertvector(f32x2_t{v0, v1}, bf16x2_t);
+        const uint32_t hb = __builtin_bit_cast(uint32_t, hp);
+        const float r0 = v0 - __uint_as_float(hb << 16), r1 = v1 - __uint_as_float(hb & 0xffff0000u);
+        const bf16x2_t mp = __builtin_convertvector(f32x2_t{r0, r1}, bf16x2_t);
+        const uint32_t mb = __builtin_bit_cast(uint32_t, mp);
+        const float s0 = r0 - __uint_as_float(mb << 16), s1 = r1 - __uint_as_float(mb & 0xffff0000u);
+        const bf16x2_t lp = __builtin_convertvector(f32x2_t{s0, s1}, bf16x2_t);
+        h[j] = hp[0];
+        h[j + 1] = hp[1];
+        m[j] = mp[0];
+        m[j + 1] = mp[1];
+        l[j] = lp[0];
+        l[j + 1] = lp[1];
     }
 }
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 /* Eight Q4_K codes, bytes 0..3 of lo then of hi (low nibbles, or the high
  * nibbles shifted down), as an exact bf16 MFMA operand. A code q in the low
@@ -1211,10 +1222,14 @@ __device__ __forceinline__ void q6_codes_bf16(uint32_t lw, uint32_t hw, int r, b
     hi = bf16x4_t{h0[0], h0[1], h1[0], h1[1]};
 }
 
-template <int M>
+/* Sub-blocks [SB0, SB0 + NSB) of a Q4_K unit (SB0 even: whole 64-weight code
+ * groups). */
+template <int M, int SB0, int NSB>
 __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
                                               f32x4_t (&acc)[4])
 {
+    static_assert(SB0 % 2 == 0 && NSB % 2 == 0 && SB0 + NSB <= 8, "whole code groups");
+    constexpr int SB1 = SB0 + NSB;
     const int kc = lane >> 4, n = lane & 15;
     const bool valid = n < M;
     /* Lanes past the batch read position 0 (in bounds): their products land
@@ -1230,19 +1245,19 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     for (int g = 0; g < 4; ++g) h[g] = ld16(rowp + g * 256);
     uint2 q[2][4]; /* codes of group c and c + 1 */
 #pragma unroll
-    for (int g = 0; g < 4; ++g) q[0][g] = *(const uint2 *)(qsp + g * 256);
+    for (int g = 0; g < 4; ++g) q[(SB0 >> 1) & 1][g] = *(const uint2 *)(qsp + (SB0 >> 1) * 2048 + g * 256);
     const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
                            (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
     float xv[2][8];
-    load_x<8>(xv[0], (gf32 *)xp);
+    load_x<8>(xv[SB0 & 1], (gf32 *)(xp + 32 * SB0));
 #pragma unroll
-    for (int sb = 0; sb < 8; ++sb) {
+    for (int sb = SB0; sb < SB1; ++sb) {
         const int c = sb >> 1;
         const bool high = sb & 1;
         /* Next sub-block's activations, and at a group's start the next
          * group's codes, load while this sub-block runs. */
-        if (sb + 1 < 8) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
-        if (!high && c + 1 < 4) {
+        if (sb + 1 < SB1) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
+        if (!high && c + 1 < SB1 / 2) {
             gu8 *nq = bytes_after(qsp + (c + 1) * 2048, acc[1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
@@ -1252,7 +1267,7 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
         bf16x8_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-            b[g] = q4_codes_bf16(after(q[c & 1][g].x, acc[g][0]), after(q[c & 1][g].y, acc[g][0]), high);
+            b[g] = q4_codes_bf16(q[c & 1][g].x, q[c & 1][g].y, high);
         f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1267,9 +1282,7 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
         for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            /* Decoded here, not hoisted: the scales of one sub-block live. */
-            const float dep = d[g][0];
-            const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep), after(h[g].w, dep)};
+            const uint4 hg = h[g];
             const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
             uint32_t scw, mw;
             if (sb < 4) {
@@ -1284,6 +1297,10 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[g][j] = fmaf(sa, d[g][j], fmaf(-sm, xs[j], acc[g][j]));
         }
+        /* Scheduling stops here: the scale decode and code conversion of a
+         * sub-block stay in it, so only one sub-block's scales are live
+         * (without a copy of each header word per sub-block to order them). */
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -1291,10 +1308,13 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
  * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
  * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
  * ql/qh words serves four of them. */
-template <int M>
+/* Pairs [PR0, PR0 + NPR) of a Q6_K unit (four sub-blocks each). */
+template <int M, int PR0, int NPR>
 __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane,
                                               f32x4_t (&acc)[4])
 {
+    static_assert(PR0 + NPR <= 4 && NPR >= 1, "pairs of one unit");
+    constexpr int T0 = 4 * PR0, T1 = 4 * (PR0 + NPR);
     const int kc = lane >> 4, n = lane & 15;
     const bool valid = n < M;
     /* Lanes past the batch read position 0; their rows are never stored. */
@@ -1309,24 +1329,25 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
     }
     /* Words of pair (G, hf) and the next pair: ql for r & 1 = 0, 1 and qh. */
     uint32_t w[2][4][3];
+    constexpr int G0 = PR0 >> 1, H0 = PR0 & 1;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        w[0][g][0] = *(const uint32_t *)(wp + 0 * 1024 + g * 256);
-        w[0][g][1] = *(const uint32_t *)(wp + 2 * 1024 + g * 256);
-        w[0][g][2] = *(const uint32_t *)(wp + 8 * 1024 + g * 256);
+        w[PR0 & 1][g][0] = *(const uint32_t *)(wp + (4 * G0 + H0) * 1024 + g * 256);
+        w[PR0 & 1][g][1] = *(const uint32_t *)(wp + (4 * G0 + 2 + H0) * 1024 + g * 256);
+        w[PR0 & 1][g][2] = *(const uint32_t *)(wp + (8 + 2 * G0 + H0) * 1024 + g * 256);
     }
     float xv[2][4];
-    load_x<4>(xv[0], (gf32 *)xp);
+    load_x<4>(xv[T0 & 1], (gf32 *)(xp + 16 * (8 * G0 + H0)));
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    for (int t = T0; t < T1; ++t) {
         const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
         const int G = pr >> 1, hf = pr & 1;
         const int j = 8 * G + 2 * r + hf;
-        if (t + 1 < 16) {
+        if (t + 1 < T1) {
             const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
             load_x<4>(xv[(t + 1) & 1], ptr_after(xp + 16 * jn, acc[0][0]));
         }
-        if (r == 0 && pr + 1 < 4) {
+        if (r == 0 && pr + 1 < PR0 + NPR) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
             gu8 *np = bytes_after(wp, acc[1][0]);
 #pragma unroll
@@ -1341,7 +1362,7 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         bf16x4_t bl[4], bh[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-            q6_codes_bf16(after(w[pr & 1][g][r & 1], acc[g][0]), after(w[pr & 1][g][2], acc[g][0]), r, bl[g], bh[g]);
+            q6_codes_bf16(w[pr & 1][g][r & 1], w[pr & 1][g][2], r, bl[g], bh[g]);
         f32x4_t d[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1362,16 +1383,58 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float s = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+            const float s = dg[g] * sbyte(word(sc[g], j >> 2), j & 3);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(s, d[g][i], acc[g][i]);
+        }
+        /* One sub-block's codes and scale live at a time (see Q4_K). */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+/* Part `part` of `parts` (1, 2 or 4; wave-uniform) of one unit: consecutive
+ * sub-blocks (Q4_K: 8 / parts, Q6_K: 16 / parts). */
+template <int FMT, int M>
+__device__ __forceinline__ void unit_part_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int part,
+                                               int parts, f32x4_t (&acc)[4])
+{
+    if constexpr (FMT == QMV_FMT_Q4_K) {
+        if (parts == 1) {
+            q4k_unit_mfma<M, 0, 8>(slab, xu, ldx, lane, acc);
+        } else if (parts == 2) {
+            if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
+            else q4k_unit_mfma<M, 4, 4>(slab, xu, ldx, lane, acc);
+        } else {
+            switch (part) {
+            case 0: q4k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc); break;
+            case 1: q4k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc); break;
+            case 2: q4k_unit_mfma<M, 4, 2>(slab, xu, ldx, lane, acc); break;
+            default: q4k_unit_mfma<M, 6, 2>(slab, xu, ldx, lane, acc); break;
+            }
+        }
+    } else {
+        if (parts == 1) {
+            q6k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
+        } else if (parts == 2) {
+            if (part == 0) q6k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc);
+            else q6k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc);
+        } else {
+            switch (part) {
+            case 0: q6k_unit_mfma<M, 0, 1>(slab, xu, ldx, lane, acc); break;
+            case 1: q6k_unit_mfma<M, 1, 1>(slab, xu, ldx, lane, acc); break;
+            case 2: q6k_unit_mfma<M, 2, 1>(slab, xu, ldx, lane, acc); break;
+            default: q6k_unit_mfma<M, 3, 1>(slab, xu, ldx, lane, acc); break;
+            }
         }
     }
 }
 
-/* Same launch plan, combine and split-K protocol as matvec_kernel; each wave
- * runs its units on the matrix cores and scatters its 64 rows x M positions
- * into the combine buffer. */
+/* Same combine and split-K protocol as matvec_kernel; each wave runs one work
+ * item on the matrix cores and scatters its 64 rows x M positions into the
+ * combine buffer. A work item is a unit, or with p.parts = 2 or 4 a part of
+ * one: a tile then has units x parts items, in unit-major order, so the
+ * waves of a small launch (or the last waves of a large one) are shorter and
+ * more of them run at once. */
 /* Four resident waves per SIMD (at most 128 VGPRs): these waves are short
  * and latency-bound, so residency matters more than registers. */
 template <int FMT, int M>
@@ -1383,17 +1446,18 @@ matvec_mfma_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgWork w = locate(p, wave);
+    const int shift = p.parts == 4 ? 2 : p.parts == 2 ? 1 : 0;
+    const WgWork w = locate(p, wave, p.units << shift);
     const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
 
     f32x4_t acc[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) acc[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int u = w.u_begin; u < w.u_end; ++u) {
-        if constexpr (FMT == QMV_FMT_Q4_K)
-            q4k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
-        else
-            q6k_unit_mfma<M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane, acc);
+    /* One work item per wave: the host plans units_per_wave = 1 here. */
+    if (w.u_begin < w.u_end) {
+        const int u = w.u_begin >> shift;
+        unit_part_mfma<FMT, M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane,
+                               w.u_begin - (u << shift), 1 << shift, acc);
     }
 
     const int kc = lane >> 4, n = lane & 15;

@@ -417,6 +417,9 @@ std::atomic<int> g_mfma_min_batch{env_int("QMV_MFMA_MIN_BATCH", 0)};
 /* QMV_PAIRED_SWIGLU=0 runs the fused SwiGLU with the tile-pair count instead
  * of paired workgroups (for comparison). */
 std::atomic<int> g_paired_swiglu{env_int("QMV_PAIRED_SWIGLU", 1)};
+/* QMV_MFMA_PARTS = 1, 2 or 4 forces the work items per unit of the
+ * matrix-core kernel (for measurement). */
+std::atomic<int> g_mfma_parts{env_int("QMV_MFMA_PARTS", 0)};
 
 bool use_matrix_cores(int fmt, int batch)
 {
@@ -439,7 +442,7 @@ struct Plan {
  * waves and stream-K partitions at every decode shape measured. With
  * target_waves set, units per wave grow instead until about that many waves
  * cover the launch. */
-Plan plan_for(long long total_tiles, int units, int long_waves)
+Plan plan_for(long long total_tiles, int units, int long_waves, int max_u = 8)
 {
     const int target = g_target_waves.load();
     const int force_u = g_force_u.load();
@@ -450,6 +453,7 @@ Plan plan_for(long long total_tiles, int units, int long_waves)
         U = (int)(u < 1 ? 1 : u > 8 ? 8 : u);
     }
     if (force_u > 0) U = force_u;
+    if (U > max_u) U = max_u;
     if (U > units) U = units;
     int W = force_w > 0 ? force_w : target > 0 ? QMV_MAX_WAVES : units >= 32 ? long_waves : 4;
     const int need = (units + U - 1) / U;
@@ -466,6 +470,19 @@ Plan plan_for(long long total_tiles, int units, int long_waves)
     p.splits = S;
     p.units_per_split = ups;
     return p;
+}
+
+/* Work items per K-unit on the matrix-core kernel (M <= 8). Measured at
+ * M = 8 on the Qwen2.5-7B layer shapes (us per launch, parts 1 / 2 / 4):
+ * q|k|v 16.2 / 13.4 / 15.0, o 13.4 / 12.8 / 14.1, gate|up 46.3 / 44.5 / 62.3,
+ * down (74 units per row) 45.1 / 51.7 / 64.6. Halves pay on rows of few
+ * units, where a unit per wave leaves about one wave per SIMD; more items
+ * cost more split-K partials than they gain. */
+int mfma_parts(int units)
+{
+    const int forced = g_mfma_parts.load();
+    if (forced == 1 || forced == 2 || forced == 4) return forced;
+    return units < 32 ? 2 : 1;
 }
 
 /* What a launch does with each tile's final rows besides storing them. */
@@ -518,7 +535,9 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         total_tiles += ts[i]->tiles;
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
-    const Plan plan = prefill ? plan_prefill(total_groups, t0->units) : plan_for(total_tiles, t0->units, batch == 1 ? 6 : 4);
+    const int parts = mfma && !prefill ? mfma_parts(t0->units) : 1;
+    const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
+                              : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, mfma ? 1 : 8);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
@@ -528,6 +547,11 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     p.cols = t0->cols;
     p.units = t0->units;
     p.units_per_wave = plan.units_per_wave;
+    p.parts = parts;
+    if (mfma && !prefill && plan.units_per_wave != 1) {
+        set_error("matrix-core launch planned with more than one work item per wave");
+        return 0;
+    }
     p.positions = batch;
     /* Fused SwiGLU at M = 1 with one unit per wave: one workgroup per
      * (tile, split) of both projections (finish_paired), when the two halves
