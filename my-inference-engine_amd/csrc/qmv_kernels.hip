@@ -1597,7 +1597,7 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
         bf16x8_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-            b[g] = q4_codes_bf16(after(q[c & 1][g].x, acc[0][g][0]), after(q[c & 1][g].y, acc[0][g][0]), high);
+            b[g] = q4_codes_bf16(q[c & 1][g].x, q[c & 1][g].y, high);
         float sa[4], sm[4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
@@ -1621,9 +1621,7 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
             if (pb == 0) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const float dep = d[g][0];
-                    const uint4 hg = {after(h[g].x, dep), after(h[g].y, dep), after(h[g].z, dep),
-                                      after(h[g].w, dep)};
+                    const uint4 hg = h[g];
                     const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
                     uint32_t scw, mw;
                     if (sb < 4) {
@@ -1643,6 +1641,8 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
                 for (int j = 0; j < 4; ++j)
                     acc[pb][g][j] = fmaf(sa[g], d[g][j], fmaf(-sm[g], xs[j], acc[pb][g][j]));
         }
+        /* One sub-block's codes and scales live at a time. */
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -1706,8 +1706,8 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
         bf16x4_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const uint32_t lw = after(w[pr & 1][g][r & 1], acc[0][g][0]);
-            const uint32_t hw = after(w[pr & 1][g][2], acc[0][g][0]);
+            const uint32_t lw = w[pr & 1][g][r & 1];
+            const uint32_t hw = w[pr & 1][g][2];
             const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
 #pragma unroll
             for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
@@ -1731,12 +1731,14 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
             for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
             if (pb == 0)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) s[g] = dg[g] * sbyte(after(word(sc[g], j >> 2), d[g][0]), j & 3);
+                for (int g = 0; g < 4; ++g) s[g] = dg[g] * sbyte(word(sc[g], j >> 2), j & 3);
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(s[g], d[g][i], acc[pb][g][i]);
         }
+        /* One sub-block's codes and scale live at a time. */
+        __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
