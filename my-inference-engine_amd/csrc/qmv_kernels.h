@@ -52,9 +52,9 @@ struct MatvecParams {
     float *partials;
     unsigned *counters; /* all zero between launches; tile t at t * QMV_COUNTER_STRIDE */
     int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
-    /* Matrix-core kernel (M <= 8): work items per unit (1, 2 or 4; 0 = 1).
-     * A tile then has units x parts items of consecutive sub-blocks, and
-     * units_per_wave / units_per_split count items. */
+    /* Matrix-core kernel (M <= 8): work items per unit (1 or 2; 0 = 1). A
+     * tile then has units x parts items of consecutive sub-blocks, and
+     * units_per_wave (1) / units_per_split count items. */
     int parts;
     int positions;    /* positions in this launch (the prefill kernel's position rows past it are padding) */
     /* Fused greedy argmax (single tensor, M = 1; result non-null): tile and

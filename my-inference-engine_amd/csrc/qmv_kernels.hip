@@ -1392,49 +1392,28 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
     }
 }
 
-/* Part `part` of `parts` (1, 2 or 4; wave-uniform) of one unit: consecutive
+/* Part `part` of `parts` (1 or 2; wave-uniform) of one unit: consecutive
  * sub-blocks (Q4_K: 8 / parts, Q6_K: 16 / parts). */
 template <int FMT, int M>
 __device__ __forceinline__ void unit_part_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int part,
                                                int parts, f32x4_t (&acc)[4])
 {
     if constexpr (FMT == QMV_FMT_Q4_K) {
-        if (parts == 1) {
-            q4k_unit_mfma<M, 0, 8>(slab, xu, ldx, lane, acc);
-        } else if (parts == 2) {
-            if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
-            else q4k_unit_mfma<M, 4, 4>(slab, xu, ldx, lane, acc);
-        } else {
-            switch (part) {
-            case 0: q4k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc); break;
-            case 1: q4k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc); break;
-            case 2: q4k_unit_mfma<M, 4, 2>(slab, xu, ldx, lane, acc); break;
-            default: q4k_unit_mfma<M, 6, 2>(slab, xu, ldx, lane, acc); break;
-            }
-        }
+        if (parts == 1) q4k_unit_mfma<M, 0, 8>(slab, xu, ldx, lane, acc);
+        else if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
+        else q4k_unit_mfma<M, 4, 4>(slab, xu, ldx, lane, acc);
     } else {
-        if (parts == 1) {
-            q6k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
-        } else if (parts == 2) {
-            if (part == 0) q6k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc);
-            else q6k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc);
-        } else {
-            switch (part) {
-            case 0: q6k_unit_mfma<M, 0, 1>(slab, xu, ldx, lane, acc); break;
-            case 1: q6k_unit_mfma<M, 1, 1>(slab, xu, ldx, lane, acc); break;
-            case 2: q6k_unit_mfma<M, 2, 1>(slab, xu, ldx, lane, acc); break;
-            default: q6k_unit_mfma<M, 3, 1>(slab, xu, ldx, lane, acc); break;
-            }
-        }
+        if (parts == 1) q6k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
+        else if (part == 0) q6k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc);
+        else q6k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc);
     }
 }
 
 /* Same combine and split-K protocol as matvec_kernel; each wave runs one work
  * item on the matrix cores and scatters its 64 rows x M positions into the
- * combine buffer. A work item is a unit, or with p.parts = 2 or 4 a part of
- * one: a tile then has units x parts items, in unit-major order, so the
- * waves of a small launch (or the last waves of a large one) are shorter and
- * more of them run at once. */
+ * combine buffer. A work item is a unit, or with p.parts = 2 half of one: a
+ * tile then has units x parts items, in unit-major order, so a launch over
+ * rows of few units has twice the waves. */
 /* Four resident waves per SIMD (at most 128 VGPRs): these waves are short
  * and latency-bound, so residency matters more than registers. */
 template <int FMT, int M>
@@ -1446,7 +1425,7 @@ matvec_mfma_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int shift = p.parts == 4 ? 2 : p.parts == 2 ? 1 : 0;
+    const int shift = p.parts == 2 ? 1 : 0;
     const WgWork w = locate(p, wave, p.units << shift);
     const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
 

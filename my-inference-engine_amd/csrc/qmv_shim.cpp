@@ -417,7 +417,7 @@ std::atomic<int> g_mfma_min_batch{env_int("QMV_MFMA_MIN_BATCH", 0)};
 /* QMV_PAIRED_SWIGLU=0 runs the fused SwiGLU with the tile-pair count instead
  * of paired workgroups (for comparison). */
 std::atomic<int> g_paired_swiglu{env_int("QMV_PAIRED_SWIGLU", 1)};
-/* QMV_MFMA_PARTS = 1, 2 or 4 forces the work items per unit of the
+/* QMV_MFMA_PARTS = 1 or 2 forces the work items per unit of the
  * matrix-core kernel (for measurement). */
 std::atomic<int> g_mfma_parts{env_int("QMV_MFMA_PARTS", 0)};
 
@@ -477,11 +477,11 @@ Plan plan_for(long long total_tiles, int units, int long_waves, int max_u = 8)
  * q|k|v 16.2 / 13.4 / 15.0, o 13.4 / 12.8 / 14.1, gate|up 46.3 / 44.5 / 62.3,
  * down (74 units per row) 45.1 / 51.7 / 64.6. Halves pay on rows of few
  * units, where a unit per wave leaves about one wave per SIMD; more items
- * cost more split-K partials than they gain. */
+ * cost more split-K partials than they gain, so quarters are not built. */
 int mfma_parts(int units)
 {
     const int forced = g_mfma_parts.load();
-    if (forced == 1 || forced == 2 || forced == 4) return forced;
+    if (forced == 1 || forced == 2) return forced;
     return units < 32 ? 2 : 1;
 }
 
