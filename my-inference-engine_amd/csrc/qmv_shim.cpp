@@ -432,7 +432,8 @@ struct Plan {
     int units_per_wave, waves, splits, units_per_split;
 };
 
-/* Default: one K-unit per wave and four waves per workgroup (one per SIMD);
+/* Default: one K-unit per wave and `short_waves` (4, one per SIMD; 5 for
+ * large single-position launches) waves per workgroup;
  * for long rows (>= 32 K-units) at M = 1, `long_waves` = 6: down 3584 x
  * 18944 Q6_K takes 14.4 us against 15.8 at 8 and 15.1 at 4, whose 19 splits
  * need two rounds of partial loads. Batches keep 4 for long rows too (down at
@@ -442,7 +443,7 @@ struct Plan {
  * waves and stream-K partitions at every decode shape measured. With
  * target_waves set, units per wave grow instead until about that many waves
  * cover the launch. */
-Plan plan_for(long long total_tiles, int units, int long_waves, int max_u = 8)
+Plan plan_for(long long total_tiles, int units, int long_waves, int short_waves, int max_u = 8)
 {
     const int target = g_target_waves.load();
     const int force_u = g_force_u.load();
@@ -455,7 +456,7 @@ Plan plan_for(long long total_tiles, int units, int long_waves, int max_u = 8)
     if (force_u > 0) U = force_u;
     if (U > max_u) U = max_u;
     if (U > units) U = units;
-    int W = force_w > 0 ? force_w : target > 0 ? QMV_MAX_WAVES : units >= 32 ? long_waves : 4;
+    int W = force_w > 0 ? force_w : target > 0 ? QMV_MAX_WAVES : units >= 32 ? long_waves : short_waves;
     const int need = (units + U - 1) / U;
     if (W > need) W = need;
     int S = (units + W * U - 1) / (W * U);
@@ -536,8 +537,15 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
     const int parts = mfma && !prefill ? mfma_parts(t0->units) : 1;
+    /* Single-position launches of many units (the vocabulary projection:
+     * 33236) run several rounds of resident waves; five waves per workgroup
+     * (three splits of 14 units instead of four) measured 80.9 us against
+     * 84.8-86.8 at four for 151936 x 3584 Q6_K, while four stays best for
+     * the decode-step launches (o 3584 x 3584: 6.0 against 6.6 us). */
+    const int short_waves = batch == 1 && total_tiles * t0->units > 16384 ? 5 : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
-                              : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, mfma ? 1 : 8);
+                              : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
+                                         mfma ? 1 : 8);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
