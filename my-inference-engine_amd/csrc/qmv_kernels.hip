@@ -645,7 +645,7 @@ __device__ __forceinline__ float unit_m1(const typename UnitOf<FMT>::T &u, const
  * beyond that each region loads after the previous one finished. */
 template <int FMT, int M, bool kGuard>
 __device__ __forceinline__ void unit_mn(const typename UnitOf<FMT>::T &u, const float *__restrict__ xu, int ldx,
-                                        int kleft, float (&acc)[M])
+                                        int kleft, float (&acc)[M], int rb, int re)
 {
     constexpr int R = RegionCount<FMT>::value;
     constexpr bool kAhead = M <= 4;
@@ -664,12 +664,14 @@ __device__ __forceinline__ void unit_mn(const typename UnitOf<FMT>::T &u, const 
         }
     };
     /* Regions are ordered by block (4 per 32-weight block for Q8_0/Q5_0); a
-     * partial last unit lacks whole blocks, since K is a multiple of 32. */
-    const int rvalid = kGuard ? (kleft / 32) * 4 : R;
-    if (kAhead) load(xr[0], 0, 0.0f, 0.0f, 0.0f);
+     * partial last unit lacks whole blocks, since K is a multiple of 32.
+     * Only regions [rb, re) run (half a unit: rb = 0 or R / 2, so rb is even
+     * and region rb's activations go to xr[0]). */
+    const int rvalid = min(kGuard ? (kleft / 32) * 4 : R, re);
+    if (kAhead) load(xr[0], rb, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        if (r < rvalid) { /* uniform; false only past K in a partial unit */
+        if (r >= rb && r < rvalid) { /* uniform */
             const float prev = all_of(acc); /* every FMA of region r-1 is done */
             if (kAhead) {
                 if (r + 1 < rvalid) load(xr[(r + 1) & 1], r + 1, xr[r & 1][0], prev, prev);
@@ -689,7 +691,8 @@ __device__ __forceinline__ void unit_mn(const typename UnitOf<FMT>::T &u, const 
 
 template <int FMT, int M>
 __device__ __forceinline__ void unit_step(const typename UnitOf<FMT>::T &u, const float *__restrict__ x, int ldx,
-                                          int cols, int unit, int lane, float (&acc)[M])
+                                          int cols, int unit, int lane, float (&acc)[M], int rb = 0,
+                                          int re = RegionCount<FMT>::value)
 {
     constexpr int UW = UnitOf<FMT>::kWeights;
     const int k0 = unit * UW;
@@ -697,10 +700,10 @@ __device__ __forceinline__ void unit_step(const typename UnitOf<FMT>::T &u, cons
     const float *xu = x + k0;
     if (UW == 256 || kleft >= UW) {
         if constexpr (M == 1) acc[0] += unit_m1<FMT, false>(u, xu, lane, kleft);
-        else unit_mn<FMT, M, false>(u, xu, ldx, kleft, acc);
+        else unit_mn<FMT, M, false>(u, xu, ldx, kleft, acc, rb, re);
     } else {
         if constexpr (M == 1) acc[0] += unit_m1<FMT, true>(u, xu, lane, kleft);
-        else unit_mn<FMT, M, true>(u, xu, ldx, kleft, acc);
+        else unit_mn<FMT, M, true>(u, xu, ldx, kleft, acc, rb, re);
     }
 }
 
@@ -1050,7 +1053,10 @@ matvec_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const WgWork w = locate(p, wave, p.units);
+    /* Batches may run half units (p.parts = 2, one work item per wave): a
+     * tile then has 2 x units items, item i being half i & 1 of unit i / 2. */
+    const int shift = M >= 2 && kOne && p.parts == 2 ? 1 : 0;
+    const WgWork w = locate(p, wave, p.units << shift);
     const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
     float acc[M];
 #pragma unroll
@@ -1058,9 +1064,12 @@ matvec_kernel(MatvecParams p)
 
     if (kOne) {
         if (w.u_begin < w.u_end) {
+            constexpr int R = RegionCount<FMT>::value;
+            const int u = w.u_begin >> shift, span = R >> shift;
+            const int rb = (w.u_begin - (u << shift)) * span;
             Unit a;
-            load_unit(a, wtile + (size_t)w.u_begin * SLAB, lane);
-            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, w.u_begin, lane, acc);
+            load_unit(a, wtile + (size_t)u * SLAB, lane);
+            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u, lane, acc, rb, rb + span);
         }
     } else if (w.u_begin < w.u_end) {
         /* Two units in flight per wave: the next unit's planes are loading

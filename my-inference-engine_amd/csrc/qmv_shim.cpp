@@ -420,6 +420,8 @@ std::atomic<int> g_paired_swiglu{env_int("QMV_PAIRED_SWIGLU", 1)};
 /* QMV_MFMA_PARTS = 1 or 2 forces the work items per unit of the
  * matrix-core kernel (for measurement). */
 std::atomic<int> g_mfma_parts{env_int("QMV_MFMA_PARTS", 0)};
+/* QMV_VALU_PARTS = 1 or 2: the same for the VALU kernels' batches. */
+std::atomic<int> g_valu_parts{env_int("QMV_VALU_PARTS", 0)};
 
 bool use_matrix_cores(int fmt, int batch)
 {
@@ -486,6 +488,22 @@ int mfma_parts(int units)
     return units < 32 ? 2 : 1;
 }
 
+/* Work items per K-unit on the VALU kernels for batches (M >= 2): halves.
+ * Beyond 4 positions a region's activations load only after the previous
+ * region's FMAs, so a unit is a long serial chain per wave; half units
+ * double the waves and halve the chain. Measured (us per launch, whole /
+ * half units): Qwen2.5-1.5B Q5_0 q|k|v and o at M = 8 13.7 / 11.9 and
+ * 13.4 / 11.6; Qwen2.5-7B Q4_K q|k|v and o at M = 4 14.1 / 11.8 and
+ * 13.3 / 11.1, at M = 2 11.0 / 9.2 and 10.4 / 8.7; the large launches
+ * (gate|up, down) within 1 us either way. */
+int valu_parts(int units)
+{
+    const int forced = g_valu_parts.load();
+    if (forced == 1 || forced == 2) return forced;
+    (void)units;
+    return 2;
+}
+
 /* What a launch does with each tile's final rows besides storing them. */
 struct Epilogue {
     const float *const *add = nullptr; /* per tensor (entries may be null): y += add */
@@ -536,7 +554,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         total_tiles += ts[i]->tiles;
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
-    const int parts = mfma && !prefill ? mfma_parts(t0->units) : 1;
+    const int parts = prefill ? 1 : mfma ? mfma_parts(t0->units) : batch >= 2 ? valu_parts(t0->units) : 1;
     /* Single-position launches of many units (the vocabulary projection:
      * 33236) run several rounds of resident waves; five waves per workgroup
      * (three splits of 14 units instead of four) measured 80.9 us against
@@ -545,7 +563,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const int short_waves = batch == 1 && total_tiles * t0->units > 16384 ? 5 : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
-                                         mfma ? 1 : 8);
+                                         mfma || parts > 1 ? 1 : 8);
 
     qmv::MatvecParams p;
     memset(&p, 0, sizeof p);
@@ -556,8 +574,8 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     p.units = t0->units;
     p.units_per_wave = plan.units_per_wave;
     p.parts = parts;
-    if (mfma && !prefill && plan.units_per_wave != 1) {
-        set_error("matrix-core launch planned with more than one work item per wave");
+    if ((mfma || parts > 1) && !prefill && plan.units_per_wave != 1) {
+        set_error("launch planned with more than one work item per wave");
         return 0;
     }
     p.positions = batch;
