@@ -246,7 +246,8 @@ int qmv_device_count(void);
  * many waves cover the launch. Q4_K and Q6_K batches of at least
  * mfma_min_batch positions (default 7 for Q4_K, 8 for Q6_K; a value above
  * QMV_MAX_BATCH turns it off, and then batches run in launches of 8 on the
- * VALU path) run on the matrix cores. Defaults may also come from the
+ * VALU path) run on the matrix cores, and so do Q5_0 launches of 5 to 8
+ * positions (QMV_Q5_MFMA_MIN_BATCH in the environment; 0 turns it off). Defaults may also come from the
  * QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP /
  * QMV_MFMA_MIN_BATCH environment variables. Any setting stays within the row
  * tolerance: the plan only changes the summation order, and a given plan

@@ -1313,6 +1313,103 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     }
 }
 
+/* Eight Q5_0 codes b - 16 of one block (b = low nibble | fifth bit << 4) as
+ * two exact bf16 operands whose sum is b - 16: the nibbles, whose bytes are
+ * the FP8 E4M3 patterns of nib * 2^-9 (scale 2^9), and 16 * (bit - 1), the
+ * E4M3 patterns of -1 and 0 picked by v_perm_b32 from the table 0xb8, 0x00
+ * with the bit as selector (scale 16). n0, n1: the nibbles of codes 0..3 and
+ * 4..7 in the low bits of each byte; bits: the eight fifth bits. */
+__device__ __forceinline__ void q5_codes_bf16(uint32_t n0, uint32_t n1, uint32_t bits, bf16x8_t &lo,
+                                              bf16x8_t &hi)
+{
+    const uint32_t s0 = ((bits & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t s1 = (((bits >> 4) & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t h0 = __builtin_amdgcn_perm(0u, 0x000000b8u, s0);
+    const uint32_t h1 = __builtin_amdgcn_perm(0u, 0x000000b8u, s1);
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(n0, 512.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(n0, 512.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(n1, 512.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(n1, 512.0f, true);
+    const bf16x2_t e = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h0, 16.0f, false);
+    const bf16x2_t f = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h0, 16.0f, true);
+    const bf16x2_t g = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h1, 16.0f, false);
+    const bf16x2_t h = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h1, 16.0f, true);
+    lo = bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    hi = bf16x8_t{e[0], e[1], f[0], f[1], g[0], g[1], h[0], h[1]};
+}
+
+/* Blocks [B0, B0 + NB) of a Q5_0 unit (four 32-weight blocks), of which the
+ * first `nvalid` lie within K (the rest of a partial last unit are zero bytes
+ * and their activations are not read). Lane (kc, n) supplies weights
+ * 8kc..8kc+7 of a block of row 16g + n: low nibbles of qs bytes 8kc.. for
+ * kc < 2, high nibbles of bytes 8(kc - 2).. for kc >= 2, and qh bits 8kc... */
+template <int M, int B0, int NB>
+__device__ __forceinline__ void q50_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int nvalid,
+                                              f32x4_t (&acc)[4])
+{
+    static_assert(B0 + NB <= 4 && NB >= 1, "blocks of one unit");
+    constexpr int B1 = B0 + NB;
+    const int kc = lane >> 4, n = lane & 15;
+    const bool valid = n < M;
+    /* Lanes past the batch read position 0; their rows are never stored. */
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
+    const uint8_t *qsp = slab + n * 16 + 8 * (kc & 1); /* + 1024 j + 256 g */
+    const int nsh = 4 * (kc >> 1), bsh = 8 * kc;
+    uint2 dw[4]; /* the four f16 d's of row 16g + n */
+    uint32_t qh[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        dw[g] = *(const uint2 *)(slab + 5120 + (16 * g + n) * 8);
+        qh[g] = *(const uint32_t *)(slab + 4096 + (16 * g + n) * 16 + 4 * B0);
+    }
+    uint2 q[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[B0 & 1][g] = *(const uint2 *)(qsp + B0 * 1024 + g * 256);
+    float xv[2][8];
+    if (B0 < nvalid) load_x<8>(xv[B0 & 1], (gf32 *)(xp + 32 * B0));
+#pragma unroll
+    for (int j = B0; j < B1; ++j) {
+        if (j >= nvalid) break; /* uniform */
+        uint32_t qhn[4];
+        if (j + 1 < B1 && j + 1 < nvalid) {
+            load_x<8>(xv[(j + 1) & 1], ptr_after(xp + 32 * (j + 1), acc[0][0]));
+            gu8 *nq = bytes_after(qsp + (j + 1) * 1024, acc[1][0]);
+            gu8 *nh = bytes_after(slab + 4096 + n * 16 + 4 * (j + 1), acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                q[(j + 1) & 1][g] = gload8(nq + g * 256);
+                qhn[g] = *(gu32 *)(nh + g * 256);
+            }
+        }
+        bf16x8_t a0, a1, a2;
+        x_limbs<8>(xv[j & 1], true, a0, a1, a2);
+        /* Row group by row group: one group's two code operands are live at
+         * a time, and its six MFMAs overlap the next group's conversion. */
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            bf16x8_t bl, bh;
+            q5_codes_bf16((q[j & 1][g].x >> nsh) & 0x0f0f0f0fu, (q[j & 1][g].y >> nsh) & 0x0f0f0f0fu,
+                          (qh[g] >> bsh) & 0xffu, bl, bh);
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bl, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bh, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bl, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bh, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bl, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bh, d, 0, 0, 0);
+            const float s = f16_bits_to_f32(word(dw[g], j >> 1) >> (16 * (j & 1)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(s, d[i], acc[g][i]);
+        }
+        if (j + 1 < B1 && j + 1 < nvalid) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) qh[g] = qhn[g];
+        }
+        /* One block's codes live at a time (as for Q4_K). */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 /* Q6_K sub-block j = 8G + 2r + hf (16 weights) takes its low nibbles from
  * ql plane 4G + 2(r & 1) + hf (>> 4 for r >= 2) and its two high bits from qh
  * plane 8 + 2G + hf (>> 2r); sub-blocks are visited by (G, hf), so one set of
@@ -1405,9 +1502,15 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
  * sub-blocks (Q4_K: 8 / parts, Q6_K: 16 / parts). */
 template <int FMT, int M>
 __device__ __forceinline__ void unit_part_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int part,
-                                               int parts, f32x4_t (&acc)[4])
+                                               int parts, int kleft, f32x4_t (&acc)[4])
 {
-    if constexpr (FMT == QMV_FMT_Q4_K) {
+    if constexpr (FMT == QMV_FMT_Q5_0) {
+        /* Q5_0 units are four 32-weight blocks; K is a multiple of 32. */
+        const int nvalid = kleft >= 128 ? 4 : kleft / 32;
+        if (parts == 1) q50_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, nvalid, acc);
+        else if (part == 0) q50_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, nvalid, acc);
+        else q50_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, nvalid, acc);
+    } else if constexpr (FMT == QMV_FMT_Q4_K) {
         if (parts == 1) q4k_unit_mfma<M, 0, 8>(slab, xu, ldx, lane, acc);
         else if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
         else q4k_unit_mfma<M, 4, 4>(slab, xu, ldx, lane, acc);
@@ -1444,8 +1547,9 @@ matvec_mfma_kernel(MatvecParams p)
     /* One work item per wave: the host plans units_per_wave = 1 here. */
     if (w.u_begin < w.u_end) {
         const int u = w.u_begin >> shift;
-        unit_part_mfma<FMT, M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * 256, p.ldx, lane,
-                               w.u_begin - (u << shift), 1 << shift, acc);
+        constexpr int UW = UnitOf<FMT>::kWeights;
+        unit_part_mfma<FMT, M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * UW, p.ldx, lane,
+                               w.u_begin - (u << shift), 1 << shift, p.cols - u * UW, acc);
     }
 
     const int kc = lane >> 4, n = lane & 15;
@@ -2178,7 +2282,7 @@ rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, f
 template <int FMT, int M>
 static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
 {
-    if constexpr (M >= 2 && (FMT == QMV_FMT_Q4_K || FMT == QMV_FMT_Q6_K)) {
+    if constexpr (M >= 2 && (FMT == QMV_FMT_Q4_K || FMT == QMV_FMT_Q6_K || FMT == QMV_FMT_Q5_0)) {
         if (p.matrix_cores) {
             hipLaunchKernelGGL((matvec_mfma_kernel<FMT, M>), dim3(grid), dim3(waves * 64), 0, s, p);
             return hipGetLastError();

@@ -423,11 +423,28 @@ std::atomic<int> g_mfma_parts{env_int("QMV_MFMA_PARTS", 0)};
 /* QMV_VALU_PARTS = 1 or 2: the same for the VALU kernels' batches. */
 std::atomic<int> g_valu_parts{env_int("QMV_VALU_PARTS", 0)};
 
+/* Q5_0 batches from this many positions run on the matrix cores (0: never).
+ * Qwen2.5-1.5B q|k|v and o (Q5_0, K = 1536), us per launch, VALU / matrix
+ * cores: M = 8 11.95 / 11.27 and 11.58 / 10.95; M = 5 9.37 / 9.27 and
+ * 9.07 / 8.93; M = 4 8.65 / 8.71; M = 2 6.93 / 7.38. */
+std::atomic<int> g_q5_mfma_min_batch{env_int("QMV_Q5_MFMA_MIN_BATCH", 5)};
+
 bool use_matrix_cores(int fmt, int batch)
 {
+    if (fmt == QMV_FMT_Q5_0) {
+        const int t = g_q5_mfma_min_batch.load();
+        return t > 0 && batch >= t && batch <= QMV_VALU_MAX_POSITIONS;
+    }
     if (fmt != QMV_FMT_Q4_K && fmt != QMV_FMT_Q6_K) return false;
     const int t = g_mfma_min_batch.load();
     return batch >= (t > 0 ? t : fmt == QMV_FMT_Q4_K ? 7 : 8);
+}
+
+/* Launches of 9..32 positions: the prefill kernel (Q4_K, Q6_K only). */
+bool use_prefill(int fmt, int batch)
+{
+    return (fmt == QMV_FMT_Q4_K || fmt == QMV_FMT_Q6_K) && batch > QMV_VALU_MAX_POSITIONS &&
+           use_matrix_cores(fmt, batch);
 }
 
 struct Plan {
@@ -544,7 +561,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
      * More: the prefill kernel, 16 or 32 position rows with the batch in the
      * first. */
     const bool prefill = batch > QMV_VALU_MAX_POSITIONS;
-    if (prefill && !mfma) {
+    if (prefill && !use_prefill(t0->geo.format, batch)) {
         set_error("more than 8 positions per launch need the matrix-core path");
         return 0;
     }
@@ -668,8 +685,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
 int chunk_positions(int fmt, int batch)
 {
     const int wide = batch < QMV_MFMA_MAX_POSITIONS ? batch : QMV_MFMA_MAX_POSITIONS;
-    return wide > QMV_VALU_MAX_POSITIONS && use_matrix_cores(fmt, wide) ? QMV_MFMA_MAX_POSITIONS
-                                                                           : QMV_VALU_MAX_POSITIONS;
+    return use_prefill(fmt, wide) ? QMV_MFMA_MAX_POSITIONS : QMV_VALU_MAX_POSITIONS;
 }
 
 /* Enqueue a batch of any size as launches of up to chunk_positions(). */
