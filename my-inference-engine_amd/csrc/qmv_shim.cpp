@@ -577,7 +577,12 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
      * (three splits of 14 units instead of four) measured 80.9 us against
      * 84.8-86.8 at four for 151936 x 3584 Q6_K, while four stays best for
      * the decode-step launches (o 3584 x 3584: 6.0 against 6.6 us). */
-    const int short_waves = batch == 1 && total_tiles * t0->units > 16384 ? 5 : 4;
+    /* Small single-position launches over rows of at most 8 units take each
+     * tile in one workgroup, with no split-K tail: Q8_0 896 x 896 (7 units)
+     * 4.80 us against 5.18-5.24 us in two splits. Longer rows keep the
+     * splits (Q6_K 896 x 4864, 19 units: 6.1 us at 4 waves, 7.4 at 7). */
+    const bool one_split = batch == 1 && t0->units <= QMV_MAX_WAVES && total_tiles * t0->units <= 2048;
+    const int short_waves = one_split ? t0->units : batch == 1 && total_tiles * t0->units > 16384 ? 5 : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
                                          mfma || parts > 1 ? 1 : 8);
