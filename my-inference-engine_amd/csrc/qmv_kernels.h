@@ -51,7 +51,7 @@ struct MatvecParams {
     int units_per_wave; /* contiguous K-units per wave */
     float *partials;
     unsigned *counters; /* all zero between launches; tile t at t * QMV_COUNTER_STRIDE */
-    int matrix_cores; /* run Q4_K/Q6_K with M >= 2 on the matrix cores */
+    int matrix_cores; /* run this launch (Q4_K, Q6_K or Q5_0, 2 <= M <= 8) on the matrix cores */
     /* Matrix-core kernel (M <= 8): work items per unit (1 or 2; 0 = 1). A
      * tile then has units x parts items of consecutive sub-blocks, and
      * units_per_wave (1) / units_per_split count items. */
