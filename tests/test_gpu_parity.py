@@ -257,6 +257,30 @@ def test_odd_shapes(qmv, oracle, gpu, t, rows, cols):
     matvec_parity(qmv, oracle, t, rows, cols, seed=rows + cols, what="odd shape")
 
 
+def _random_cases(n, seed):
+    """Seeded shapes across every launch-plan branch: rows off the 64-row tile,
+    short and long rows (one to 40 super-blocks, or 1 to 80 blocks of 32 with
+    partial 4-block units), and batches of 1 to 40 (VALU half units, matrix
+    cores, prefill launches, chunks past 32)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        t = B.ALL_TYPES[i % len(B.ALL_TYPES)]
+        rows = int(rng.integers(1, 700))
+        if t in (B.Q4_K, B.Q6_K):
+            cols = 256 * int(rng.integers(1, 41))
+        else:
+            cols = 32 * int(rng.integers(1, 81))
+        batch = int(rng.choice([1, 1, 2, 3, 4, 5, 6, 7, 8, 9, 16, 17, 31, 32, 33, 40]))
+        cases.append((t, rows, cols, batch, 5000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("t,rows,cols,batch,seed", _random_cases(48, 2026))
+def test_random_shapes_match_oracle(qmv, oracle, gpu, t, rows, cols, batch, seed):
+    matvec_parity(qmv, oracle, t, rows, cols, batch=batch, seed=seed, what=f"random {rows}x{cols} M={batch}")
+
+
 @pytest.mark.parametrize("t", B.ALL_TYPES)
 @pytest.mark.parametrize("batch", [1, 8, 20])
 @pytest.mark.parametrize("scale", ["1e-28", "1e28", "mixed"])
