@@ -1563,7 +1563,7 @@ matvec_mfma_kernel(MatvecParams p)
     finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
 }
 
-/* ---- Prefill batches (9..32 positions), Q4_K / Q6_K: GEMM-shaped -----------
+/* ---- Prefill batches (9..32 positions), Q4_K / Q6_K / Q5_0: GEMM-shaped ----
  * A workgroup of four waves owns four consecutive 64-row tiles of one tensor
  * (one per wave) and a range of K-units. For each unit the 256 threads stage
  * the unit's activations of all positions once, as the three bf16 limbs (see
@@ -1602,8 +1602,8 @@ __device__ __forceinline__ int lds_off_after(int off, float dep)
 /* LDS image of one unit: fragment (limb L, position block pb, k-block b) is
  * 64 lanes x KL bf16, lane 16 kc + n holding A[n][KL kc .. KL kc + KL - 1] =
  * limb L of x[16 pb + n][4 KL b + KL kc ..]. */
-template <int KL, int P> struct PfLayout {
-    static constexpr int kBlocks = 256 / (4 * KL);     /* 8 (Q4_K) or 16 (Q6_K) */
+template <int KL, int P, int UW = 256> struct PfLayout {
+    static constexpr int kBlocks = UW / (4 * KL);      /* 8 (Q4_K), 16 (Q6_K) or 4 (Q5_0) */
     static constexpr int kFrag = 64 * 2 * KL;          /* bytes per fragment */
     static constexpr int kChunks = P * kBlocks * 64;   /* (pb, b, lane) chunks of KL activations */
     static constexpr int kPerThread = kChunks / (QMV_PF_WAVES * 64);
@@ -1611,31 +1611,35 @@ template <int KL, int P> struct PfLayout {
     __device__ static int offset(int limb, int pb, int b) { return ((limb * P + pb) * kBlocks + b) * kFrag; }
 };
 
-/* Chunk c of a unit: lane = c % 64, block b, position block pb. */
-template <int KL, int P>
+/* Chunk c of a unit: lane = c % 64, block b, position block pb. Blocks from
+ * kleft on (past K in a partial last Q5_0 unit) are not read and stage
+ * zeros. */
+template <int KL, int P, int UW = 256>
 __device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, int tid,
-                                          float (&xr)[PfLayout<KL, P>::kPerThread][KL])
+                                          float (&xr)[PfLayout<KL, P, UW>::kPerThread][KL], int kleft = UW)
 {
-    using L = PfLayout<KL, P>;
+    using L = PfLayout<KL, P, UW>;
 #pragma unroll
     for (int i = 0; i < L::kPerThread; ++i) {
         const int c = tid + i * QMV_PF_WAVES * 64;
         const int lane = c & 63, rest = c >> 6, b = rest % L::kBlocks, pb = rest / L::kBlocks;
         const int kc = lane >> 4, n = lane & 15, pos = 16 * pb + n;
+        const bool in_k = UW == 256 || 4 * KL * b < kleft; /* K is a multiple of 256 for K-quants */
         /* Rows past the batch read position 0 (in bounds) and stage zeros. */
-        const float *src = xu + (size_t)(pos < npos ? pos : 0) * ldx + 4 * KL * b + KL * kc;
+        const float *src = xu + (size_t)(pos < npos ? pos : 0) * ldx + (in_k ? 4 * KL * b + KL * kc : 0);
         float v[KL];
 #pragma unroll
         for (int j = 0; j < KL; ++j) v[j] = src[j];
 #pragma unroll
-        for (int j = 0; j < KL; ++j) xr[i][j] = pos < npos ? v[j] : 0.0f;
+        for (int j = 0; j < KL; ++j) xr[i][j] = pos < npos && in_k ? v[j] : 0.0f;
     }
 }
 
-template <int KL, int P>
-__device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid, const float (&xr)[PfLayout<KL, P>::kPerThread][KL])
+template <int KL, int P, int UW = 256>
+__device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid,
+                                               const float (&xr)[PfLayout<KL, P, UW>::kPerThread][KL])
 {
-    using L = PfLayout<KL, P>;
+    using L = PfLayout<KL, P, UW>;
     typedef __bf16 frag_t __attribute__((__vector_size__(KL * sizeof(__bf16))));
 #pragma unroll
     for (int i = 0; i < L::kPerThread; ++i) {
@@ -1841,6 +1845,83 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
     }
 }
 
+/* Q5_0: the unit's four blocks against the staged activations, each block's
+ * two code operands (q5_codes_bf16) converted once for every position block.
+ * dw (the four d's), qh (the four qh words) and q0 (block 0's codes) hold
+ * this unit's on entry and those of `next` on return (as for Q4_K). Blocks
+ * from nvalid on lie past K (zero bytes, zeros staged) and are skipped. */
+template <int P>
+__device__ __forceinline__ void q50_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
+                                            int nvalid, f32x4_t (&acc)[P][4], uint2 (&dw)[4], uint4 (&qh)[4],
+                                            uint2 (&q0)[4])
+{
+    using L = PfLayout<8, P, 128>;
+    const int kc = lane >> 4, n = lane & 15;
+    const int qoff = n * 16 + 8 * (kc & 1); /* + 1024 j + 256 g */
+    const uint8_t *qsp = slab + qoff;
+    const int nsh = 4 * (kc >> 1), bsh = 8 * kc;
+    uint2 q[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[0][g] = q0[g];
+    uint2 dn[4], qn[4];
+    uint4 hn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j + 1 < 4) {
+            gu8 *nq = bytes_after(qsp + (j + 1) * 1024, acc[0][1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) q[(j + 1) & 1][g] = gload8(nq + g * 256);
+        }
+        if (j == 2) {
+            gu8 *np = bytes_after(next, acc[0][2][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                dn[g] = gload8(np + 5120 + (16 * g + n) * 8);
+                hn[g] = gload16(np + 4096 + (16 * g + n) * 16);
+                qn[g] = gload8(np + qoff + g * 256);
+            }
+        }
+        if (j < nvalid) { /* uniform */
+            bf16x8_t bl[4], bh[4];
+            float sd[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                q5_codes_bf16((q[j & 1][g].x >> nsh) & 0x0f0f0f0fu, (q[j & 1][g].y >> nsh) & 0x0f0f0f0fu,
+                              (word(qh[g], j) >> bsh) & 0xffu, bl[g], bh[g]);
+                sd[g] = f16_bits_to_f32(word(dw[g], j >> 1) >> (16 * (j & 1)));
+            }
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb) {
+                typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
+                const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
+                const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, j));
+                const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, j));
+                const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, j));
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bl[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bh[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bl[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bh[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bl[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bh[g], d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(sd[g], d[i], acc[pb][g][i]);
+                }
+            }
+        }
+        /* One block's codes live at a time. */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        dw[g] = dn[g];
+        qh[g] = hn[g];
+        q0[g] = qn[g];
+    }
+}
+
 /* The workgroup's place in a prefill launch: job, tile group, K-split; this
  * wave's tile is 4 * group + wave (it may lie past the job's last tile, and
  * then the wave only helps stage). */
@@ -1953,12 +2034,15 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
 template <int FMT, int P>
 __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams p)
 {
-    constexpr int KL = FMT == QMV_FMT_Q4_K ? 8 : 4;
+    constexpr int KL = FMT == QMV_FMT_Q6_K ? 4 : 8;
     constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
+    constexpr int UW = UnitOf<FMT>::kWeights;
     constexpr int MP = 16 * P; /* position rows of the launch */
-    using L = PfLayout<KL, P>;
-    static_assert(QMV_PF_WAVES * MP * 64 * 4 <= L::kBytes, "combine buffer reuses the staging buffer");
-    __shared__ __attribute__((aligned(16))) uint8_t lds_buf[L::kBytes];
+    using L = PfLayout<KL, P, UW>;
+    /* The combine buffer (each wave's tile, MP x 64 floats) reuses the
+     * staging buffer. */
+    constexpr int kLds = L::kBytes > QMV_PF_WAVES * MP * 64 * 4 ? L::kBytes : QMV_PF_WAVES * MP * 64 * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_buf[kLds];
     lds_u8 *lds = (lds_u8 *)lds_buf;
 
     const int tid = threadIdx.x;
@@ -1979,10 +2063,17 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
 
     /* First unit's weights (this wave's tile) and activations. */
     uint4 h[4];
-    uint2 q0[4];
+    uint2 q0[4], dw[4];
     uint32_t dgw[4], w0[4][3];
     const uint8_t *first = wtile + (size_t)w.u_begin * SLAB;
-    if constexpr (FMT == QMV_FMT_Q4_K) {
+    if constexpr (FMT == QMV_FMT_Q5_0) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            dw[g] = *(const uint2 *)(first + 5120 + (16 * g + n) * 8);
+            h[g] = ld16(first + 4096 + (16 * g + n) * 16);
+            q0[g] = *(const uint2 *)(first + n * 16 + 8 * (kc & 1) + g * 256);
+        }
+    } else if constexpr (FMT == QMV_FMT_Q4_K) {
         const int qoff = (1 + (kc >> 1)) * 1024 + n * 16 + 8 * (kc & 1);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -2001,20 +2092,25 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
         }
     }
     float xr[L::kPerThread][KL];
-    pf_load_x<KL, P>(p.x + (size_t)w.u_begin * 256, p.ldx, npos, tid, xr);
+    pf_load_x<KL, P, UW>(p.x + (size_t)w.u_begin * UW, p.ldx, npos, tid, xr, p.cols - w.u_begin * UW);
 
     for (int u = w.u_begin; u < w.u_end; ++u) {
         __syncthreads(); /* every wave is done with the previous unit's image */
-        pf_store_limbs<KL, P>(lds, tid, xr);
+        pf_store_limbs<KL, P, UW>(lds, tid, xr);
         __syncthreads();
-        if (u + 1 < w.u_end) pf_load_x<KL, P>(p.x + (size_t)(u + 1) * 256, p.ldx, npos, tid, xr);
+        if (u + 1 < w.u_end)
+            pf_load_x<KL, P, UW>(p.x + (size_t)(u + 1) * UW, p.ldx, npos, tid, xr, p.cols - (u + 1) * UW);
         const uint8_t *slab = wtile + (size_t)u * SLAB;
         const uint8_t *next = u + 1 < w.u_end ? slab + SLAB : slab;
         if (active) {
-            if constexpr (FMT == QMV_FMT_Q4_K)
+            if constexpr (FMT == QMV_FMT_Q5_0) {
+                const int kleft = p.cols - u * UW; /* K is a multiple of 32 */
+                q50_unit_pf<P>(slab, next, lds, lane, kleft >= 128 ? 4 : kleft / 32, acc, dw, h, q0);
+            } else if constexpr (FMT == QMV_FMT_Q4_K) {
                 q4k_unit_pf<P>(slab, next, lds, lane, acc, h, q0);
-            else
+            } else {
                 q6k_unit_pf<P>(slab, next, lds, lane, acc, h, dgw, w0);
+            }
         }
     }
 
@@ -2382,6 +2478,8 @@ hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hi
     else if (fmt == QMV_FMT_Q4_K && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q4_K, 2>), g, b, 0, s, p);
     else if (fmt == QMV_FMT_Q6_K && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q6_K, 1>), g, b, 0, s, p);
     else if (fmt == QMV_FMT_Q6_K && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q6_K, 2>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q5_0 && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q5_0, 1>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q5_0 && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q5_0, 2>), g, b, 0, s, p);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -440,11 +440,15 @@ bool use_matrix_cores(int fmt, int batch)
     return batch >= (t > 0 ? t : fmt == QMV_FMT_Q4_K ? 7 : 8);
 }
 
-/* Launches of 9..32 positions: the prefill kernel (Q4_K, Q6_K only). */
+/* QMV_Q5_PREFILL=0 keeps Q5_0 batches in launches of 8 positions. */
+std::atomic<int> g_q5_prefill{env_int("QMV_Q5_PREFILL", 1)};
+
+/* Launches of 9..32 positions: the prefill kernel (Q4_K, Q6_K, Q5_0). */
 bool use_prefill(int fmt, int batch)
 {
-    return (fmt == QMV_FMT_Q4_K || fmt == QMV_FMT_Q6_K) && batch > QMV_VALU_MAX_POSITIONS &&
-           use_matrix_cores(fmt, batch);
+    if (batch <= QMV_VALU_MAX_POSITIONS) return false;
+    if (fmt == QMV_FMT_Q5_0) return g_q5_prefill.load() != 0;
+    return (fmt == QMV_FMT_Q4_K || fmt == QMV_FMT_Q6_K) && use_matrix_cores(fmt, batch);
 }
 
 struct Plan {
