@@ -63,8 +63,8 @@ int qmv_tensor_matvec_f32(const QmvTensorView *matrix, const float *input,
  * outputs[B,N] = inputs[B,K] * W^T for token-major batches. Replaces
  * quantized_tensor_matmul_f32 (src/quantized_matvec.h:43-50,
  * src/quantized_matvec.cpp:164-224). batch_count must be positive; each
- * pass over the weights serves up to QMV_MAX_BATCH positions (Q4_K, Q6_K
- * and Q5_0, on the matrix cores) or 8 (Q8_0).
+ * pass over the weights serves up to QMV_MAX_BATCH positions (on the
+ * matrix cores).
  */
 int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs,
                           int input_count, int batch_count, float *outputs,
@@ -126,9 +126,8 @@ int qmv_device_tensor_info(qmv_device_tensor tensor, int *rows, int *columns,
 /*
  * d_outputs[B,N] = d_inputs[B,K] * W^T with device pointers, enqueued on
  * stream without host synchronisation (1 <= batch_count <= QMV_MAX_BATCH).
- * Q4_K, Q6_K and Q5_0 batches of 9 to 32 positions (prefill chunks larger
- * than the reference's 8, src/qwen2_internal.h:7) read the weights once, on
- * the matrix cores; Q8_0 batches run in launches of 8.
+ * Batches of 9 to 32 positions (prefill chunks larger than the reference's
+ * 8, src/qwen2_internal.h:7) read the weights once, on the matrix cores.
  */
 int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_inputs,
                           int batch_count, float *d_outputs, void *stream);
@@ -249,7 +248,8 @@ int qmv_device_count(void);
  * mfma_min_batch positions (default 7 for Q4_K, 8 for Q6_K; a value above
  * QMV_MAX_BATCH turns it off, and then batches run in launches of 8 on the
  * VALU path) run on the matrix cores, and so do Q5_0 launches of 5 to 8
- * positions (QMV_Q5_MFMA_MIN_BATCH in the environment; 0 turns it off). Defaults may also come from the
+ * positions and Q8_0 launches of 4 to 8 (QMV_Q5_MFMA_MIN_BATCH /
+ * QMV_Q8_MFMA_MIN_BATCH in the environment; 0 turns them off). Defaults may also come from the
  * QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP /
  * QMV_MFMA_MIN_BATCH environment variables. Any setting stays within the row
  * tolerance: the plan only changes the summation order, and a given plan

@@ -1313,6 +1313,69 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     }
 }
 
+/* Eight Q8_0 codes (the signed bytes of lo, then of hi) as one exact bf16
+ * operand: each byte widens to fp32 with a sign-extending conversion, and
+ * pairs round to bf16 exactly (|q| <= 128 needs at most 8 significant
+ * bits). */
+__device__ __forceinline__ bf16x8_t q8_codes_bf16(uint32_t lo, uint32_t hi)
+{
+    const bf16x2_t a = __builtin_convertvector(f32x2_t{sbyte(lo, 0), sbyte(lo, 1)}, bf16x2_t);
+    const bf16x2_t b = __builtin_convertvector(f32x2_t{sbyte(lo, 2), sbyte(lo, 3)}, bf16x2_t);
+    const bf16x2_t c = __builtin_convertvector(f32x2_t{sbyte(hi, 0), sbyte(hi, 1)}, bf16x2_t);
+    const bf16x2_t d = __builtin_convertvector(f32x2_t{sbyte(hi, 2), sbyte(hi, 3)}, bf16x2_t);
+    return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+/* Blocks [B0, B0 + NB) of a Q8_0 unit (four 32-weight blocks; block j's
+ * codes 0..15 in plane 2j, 16..31 in plane 2j + 1), of which the first
+ * `nvalid` lie within K. Lane (kc, n) supplies codes 8kc..8kc+7 of a block
+ * of row 16g + n: plane 2j + kc / 2, bytes 8 (kc & 1)... */
+template <int M, int B0, int NB>
+__device__ __forceinline__ void q80_unit_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int nvalid,
+                                              f32x4_t (&acc)[4])
+{
+    static_assert(B0 + NB <= 4 && NB >= 1, "blocks of one unit");
+    constexpr int B1 = B0 + NB;
+    const int kc = lane >> 4, n = lane & 15;
+    const bool valid = n < M;
+    /* Lanes past the batch read position 0; their rows are never stored. */
+    const float *xp = xu + (size_t)(valid ? n : 0) * ldx + 8 * kc;
+    const uint8_t *qsp = slab + (kc >> 1) * 1024 + n * 16 + 8 * (kc & 1); /* + 2048 j + 256 g */
+    uint2 dw[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) dw[g] = *(const uint2 *)(slab + 8192 + (16 * g + n) * 8);
+    uint2 q[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[B0 & 1][g] = *(const uint2 *)(qsp + B0 * 2048 + g * 256);
+    float xv[2][8];
+    if (B0 < nvalid) load_x<8>(xv[B0 & 1], (gf32 *)(xp + 32 * B0));
+#pragma unroll
+    for (int j = B0; j < B1; ++j) {
+        if (j >= nvalid) break; /* uniform */
+        if (j + 1 < B1 && j + 1 < nvalid) {
+            load_x<8>(xv[(j + 1) & 1], ptr_after(xp + 32 * (j + 1), acc[0][0]));
+            gu8 *nq = bytes_after(qsp + (j + 1) * 2048, acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) q[(j + 1) & 1][g] = gload8(nq + g * 256);
+        }
+        bf16x8_t a0, a1, a2;
+        x_limbs<8>(xv[j & 1], true, a0, a1, a2);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const bf16x8_t b = q8_codes_bf16(q[j & 1][g].x, q[j & 1][g].y);
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b, d, 0, 0, 0);
+            const float sc = f16_bits_to_f32(word(dw[g], j >> 1) >> (16 * (j & 1)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(sc, d[i], acc[g][i]);
+        }
+        /* One block's codes live at a time (as for Q4_K). */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 /* Eight Q5_0 codes b - 16 of one block (b = low nibble | fifth bit << 4) as
  * two exact bf16 operands whose sum is b - 16: the nibbles, whose bytes are
  * the FP8 E4M3 patterns of nib * 2^-9 (scale 2^9), and 16 * (bit - 1), the
@@ -1504,12 +1567,18 @@ template <int FMT, int M>
 __device__ __forceinline__ void unit_part_mfma(const uint8_t *slab, const float *xu, int ldx, int lane, int part,
                                                int parts, int kleft, f32x4_t (&acc)[4])
 {
-    if constexpr (FMT == QMV_FMT_Q5_0) {
-        /* Q5_0 units are four 32-weight blocks; K is a multiple of 32. */
+    if constexpr (FMT == QMV_FMT_Q5_0 || FMT == QMV_FMT_Q8_0) {
+        /* Q5_0 / Q8_0 units are four 32-weight blocks; K is a multiple of 32. */
         const int nvalid = kleft >= 128 ? 4 : kleft / 32;
-        if (parts == 1) q50_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, nvalid, acc);
-        else if (part == 0) q50_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, nvalid, acc);
-        else q50_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, nvalid, acc);
+        if constexpr (FMT == QMV_FMT_Q5_0) {
+            if (parts == 1) q50_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, nvalid, acc);
+            else if (part == 0) q50_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, nvalid, acc);
+            else q50_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, nvalid, acc);
+        } else {
+            if (parts == 1) q80_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, nvalid, acc);
+            else if (part == 0) q80_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, nvalid, acc);
+            else q80_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, nvalid, acc);
+        }
     } else if constexpr (FMT == QMV_FMT_Q4_K) {
         if (parts == 1) q4k_unit_mfma<M, 0, 8>(slab, xu, ldx, lane, acc);
         else if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
@@ -1563,7 +1632,7 @@ matvec_mfma_kernel(MatvecParams p)
     finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
 }
 
-/* ---- Prefill batches (9..32 positions), Q4_K / Q6_K / Q5_0: GEMM-shaped ----
+/* ---- Prefill batches (9..32 positions), all four formats: GEMM-shaped -------
  * A workgroup of four waves owns four consecutive 64-row tiles of one tensor
  * (one per wave) and a range of K-units. For each unit the 256 threads stage
  * the unit's activations of all positions once, as the three bf16 limbs (see
@@ -1845,6 +1914,71 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
     }
 }
 
+/* Q8_0: as q50_unit_pf with one code operand per block (q8_codes_bf16); dw
+ * and q0 (block 0's codes) carry over to `next`. */
+template <int P>
+__device__ __forceinline__ void q80_unit_pf(const uint8_t *slab, const uint8_t *next, const lds_u8 *lds, int lane,
+                                            int nvalid, f32x4_t (&acc)[P][4], uint2 (&dw)[4], uint2 (&q0)[4])
+{
+    using L = PfLayout<8, P, 128>;
+    const int kc = lane >> 4, n = lane & 15;
+    const int qoff = (kc >> 1) * 1024 + n * 16 + 8 * (kc & 1); /* + 2048 j + 256 g */
+    const uint8_t *qsp = slab + qoff;
+    uint2 q[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[0][g] = q0[g];
+    uint2 dn[4], qn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j + 1 < 4) {
+            gu8 *nq = bytes_after(qsp + (j + 1) * 2048, acc[0][1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) q[(j + 1) & 1][g] = gload8(nq + g * 256);
+        }
+        if (j == 2) {
+            gu8 *np = bytes_after(next, acc[0][2][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                dn[g] = gload8(np + 8192 + (16 * g + n) * 8);
+                qn[g] = gload8(np + qoff + g * 256);
+            }
+        }
+        if (j < nvalid) { /* uniform */
+            bf16x8_t b[4];
+            float sd[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                b[g] = q8_codes_bf16(q[j & 1][g].x, q[j & 1][g].y);
+                sd[g] = f16_bits_to_f32(word(dw[g], j >> 1) >> (16 * (j & 1)));
+            }
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb) {
+                typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
+                const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
+                const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, j));
+                const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, j));
+                const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, j));
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(sd[g], d[i], acc[pb][g][i]);
+                }
+            }
+        }
+        /* One block's codes live at a time. */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        dw[g] = dn[g];
+        q0[g] = qn[g];
+    }
+}
+
 /* Q5_0: the unit's four blocks against the staged activations, each block's
  * two code operands (q5_codes_bf16) converted once for every position block.
  * dw (the four d's), qh (the four qh words) and q0 (block 0's codes) hold
@@ -2066,7 +2200,13 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
     uint2 q0[4], dw[4];
     uint32_t dgw[4], w0[4][3];
     const uint8_t *first = wtile + (size_t)w.u_begin * SLAB;
-    if constexpr (FMT == QMV_FMT_Q5_0) {
+    if constexpr (FMT == QMV_FMT_Q8_0) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            dw[g] = *(const uint2 *)(first + 8192 + (16 * g + n) * 8);
+            q0[g] = *(const uint2 *)(first + (kc >> 1) * 1024 + n * 16 + 8 * (kc & 1) + g * 256);
+        }
+    } else if constexpr (FMT == QMV_FMT_Q5_0) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             dw[g] = *(const uint2 *)(first + 5120 + (16 * g + n) * 8);
@@ -2103,9 +2243,11 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
         const uint8_t *slab = wtile + (size_t)u * SLAB;
         const uint8_t *next = u + 1 < w.u_end ? slab + SLAB : slab;
         if (active) {
-            if constexpr (FMT == QMV_FMT_Q5_0) {
+            if constexpr (FMT == QMV_FMT_Q5_0 || FMT == QMV_FMT_Q8_0) {
                 const int kleft = p.cols - u * UW; /* K is a multiple of 32 */
-                q50_unit_pf<P>(slab, next, lds, lane, kleft >= 128 ? 4 : kleft / 32, acc, dw, h, q0);
+                const int nvalid = kleft >= 128 ? 4 : kleft / 32;
+                if constexpr (FMT == QMV_FMT_Q5_0) q50_unit_pf<P>(slab, next, lds, lane, nvalid, acc, dw, h, q0);
+                else q80_unit_pf<P>(slab, next, lds, lane, nvalid, acc, dw, q0);
             } else if constexpr (FMT == QMV_FMT_Q4_K) {
                 q4k_unit_pf<P>(slab, next, lds, lane, acc, h, q0);
             } else {
@@ -2378,7 +2520,7 @@ rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, f
 template <int FMT, int M>
 static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
 {
-    if constexpr (M >= 2 && (FMT == QMV_FMT_Q4_K || FMT == QMV_FMT_Q6_K || FMT == QMV_FMT_Q5_0)) {
+    if constexpr (M >= 2) {
         if (p.matrix_cores) {
             hipLaunchKernelGGL((matvec_mfma_kernel<FMT, M>), dim3(grid), dim3(waves * 64), 0, s, p);
             return hipGetLastError();
@@ -2480,6 +2622,8 @@ hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hi
     else if (fmt == QMV_FMT_Q6_K && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q6_K, 2>), g, b, 0, s, p);
     else if (fmt == QMV_FMT_Q5_0 && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q5_0, 1>), g, b, 0, s, p);
     else if (fmt == QMV_FMT_Q5_0 && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q5_0, 2>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q8_0 && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q8_0, 1>), g, b, 0, s, p);
+    else if (fmt == QMV_FMT_Q8_0 && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q8_0, 2>), g, b, 0, s, p);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

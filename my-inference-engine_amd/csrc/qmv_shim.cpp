@@ -429,10 +429,16 @@ std::atomic<int> g_valu_parts{env_int("QMV_VALU_PARTS", 0)};
  * 9.07 / 8.93; M = 4 8.65 / 8.71; M = 2 6.93 / 7.38. */
 std::atomic<int> g_q5_mfma_min_batch{env_int("QMV_Q5_MFMA_MIN_BATCH", 5)};
 
+/* Q8_0 batches from this many positions run on the matrix cores (0: never).
+ * Q8_0 896 x 896 and 4864 x 896, us per launch, VALU / matrix cores: M = 8
+ * 11.03 / 9.82 and 11.74 / 10.51; M = 4 7.97 / 7.56 and 8.34 / 8.20; M = 2
+ * 6.44 / 6.25 and 6.72 / 6.95. */
+std::atomic<int> g_q8_mfma_min_batch{env_int("QMV_Q8_MFMA_MIN_BATCH", 4)};
+
 bool use_matrix_cores(int fmt, int batch)
 {
-    if (fmt == QMV_FMT_Q5_0) {
-        const int t = g_q5_mfma_min_batch.load();
+    if (fmt == QMV_FMT_Q5_0 || fmt == QMV_FMT_Q8_0) {
+        const int t = (fmt == QMV_FMT_Q5_0 ? g_q5_mfma_min_batch : g_q8_mfma_min_batch).load();
         return t > 0 && batch >= t && batch <= QMV_VALU_MAX_POSITIONS;
     }
     if (fmt != QMV_FMT_Q4_K && fmt != QMV_FMT_Q6_K) return false;
@@ -440,14 +446,17 @@ bool use_matrix_cores(int fmt, int batch)
     return batch >= (t > 0 ? t : fmt == QMV_FMT_Q4_K ? 7 : 8);
 }
 
-/* QMV_Q5_PREFILL=0 keeps Q5_0 batches in launches of 8 positions. */
+/* QMV_Q5_PREFILL=0 / QMV_Q8_PREFILL=0 keep Q5_0 / Q8_0 batches in launches
+ * of 8 positions. */
 std::atomic<int> g_q5_prefill{env_int("QMV_Q5_PREFILL", 1)};
+std::atomic<int> g_q8_prefill{env_int("QMV_Q8_PREFILL", 1)};
 
-/* Launches of 9..32 positions: the prefill kernel (Q4_K, Q6_K, Q5_0). */
+/* Launches of 9..32 positions: the prefill kernel (all four formats). */
 bool use_prefill(int fmt, int batch)
 {
     if (batch <= QMV_VALU_MAX_POSITIONS) return false;
     if (fmt == QMV_FMT_Q5_0) return g_q5_prefill.load() != 0;
+    if (fmt == QMV_FMT_Q8_0) return g_q8_prefill.load() != 0;
     return (fmt == QMV_FMT_Q4_K || fmt == QMV_FMT_Q6_K) && use_matrix_cores(fmt, batch);
 }
 

@@ -61,7 +61,7 @@ def test_prefill_batches_match_oracle(qmv, oracle, gpu, t, batch):
 
 @pytest.mark.parametrize("t,rows,cols", [(B.Q4_K, 18944, 3584), (B.Q6_K, 3584, 18944), (B.Q4_K, 3584, 3584),
                                          (B.Q4_K, 512, 3584), (B.Q4_K, 8960, 1536), (B.Q5_0, 1536, 1536),
-                                         (B.Q5_0, 256, 1536)])
+                                         (B.Q5_0, 256, 1536), (B.Q8_0, 896, 896), (B.Q8_0, 4864, 896)])
 def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
     batch = 32
     raw = qmv.synth_tensor(t, rows, cols, seed=310)
@@ -72,7 +72,7 @@ def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
     qmv.release_tensor(v.data)
 
 
-@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q5_0])
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q5_0, B.Q8_0])
 @pytest.mark.parametrize("batch,parts", [(32, [16, 16]), (27, [9, 18]), (24, [12, 12]), (30, [10, 10, 10])])
 def test_prefill_positions_independent(qmv, gpu, hip, t, batch, parts):
     """One prefill launch of `batch` positions against the same positions in
@@ -167,7 +167,7 @@ def test_device_batch_limit(qmv, gpu, hip):
     dt.close()
 
 
-@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q5_0])
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q5_0, B.Q8_0])
 @pytest.mark.parametrize("rows,cols,batch", [(1, 256, 9), (63, 512, 32), (130, 256, 17), (65, 2304, 12),
                                              (257, 1024, 31)])
 def test_prefill_edge_shapes(qmv, oracle, gpu, t, rows, cols, batch):
@@ -181,16 +181,16 @@ def test_prefill_edge_shapes(qmv, oracle, gpu, t, rows, cols, batch):
     qmv.release_tensor(v.data)
 
 
+@pytest.mark.parametrize("t", [B.Q5_0, B.Q8_0])
 @pytest.mark.parametrize("rows,cols,batch", [(130, 96, 17), (65, 7 * 32 + 512, 12), (200, 32, 32), (64, 1568, 25)])
-def test_prefill_q5_0_partial_units(qmv, oracle, gpu, rows, cols, batch):
-    """Q5_0 rows whose last 4-block unit is partial (K = 32 * odd): the
-    blocks past K are skipped and no activation past K is read."""
-    t = B.Q5_0
+def test_prefill_partial_units(qmv, oracle, gpu, t, rows, cols, batch):
+    """Q5_0 / Q8_0 rows whose last 4-block unit is partial (K = 32 * odd):
+    the blocks past K are skipped and no activation past K is read."""
     raw = qmv.synth_tensor(t, rows, cols, seed=370 + rows)
     x = qmv.synth_normal(batch * cols, seed=371 + rows).reshape(batch, cols)
     v = qmv.make_view(raw, t, rows, cols)
     y = qmv.matvec(v, x)
-    _check(oracle, raw, t, rows, cols, x, y, f"Q5_0 {rows}x{cols} B={batch}")
+    _check(oracle, raw, t, rows, cols, x, y, f"type {t} {rows}x{cols} B={batch}")
     qmv.release_tensor(v.data)
 
 
