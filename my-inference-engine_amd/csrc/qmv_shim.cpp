@@ -547,12 +547,14 @@ struct Epilogue {
  * (M = 32): five units per split for long rows (down, 74 units: 74 us
  * against 100 us at two) and for launches of many tile groups (gate|up, 148
  * groups: 64 us against 77 us at two); two for small launches (q|k|v, o:
- * 28 and 27 us against 41 at five), where more splits keep more CUs busy.
+ * 28 and 27 us against 41 at five), where more splits keep more CUs busy;
+ * one for rows of at most 8 units in at most 8 tile groups (Q8_0 896 x 896:
+ * 17.8 us against 19.3 at two for 32 positions, 11.2 against 12.8 for 16).
  * units_per_wave, when forced, sets the units per split instead. */
 Plan plan_prefill(long long groups, int units)
 {
     const int force_u = g_force_u.load();
-    int ups = force_u > 0 ? force_u : units >= 32 || groups >= 100 ? 5 : 2;
+    int ups = force_u > 0 ? force_u : units >= 32 || groups >= 100 ? 5 : units <= 8 && groups <= 8 ? 1 : 2;
     if (ups > units) ups = units;
     Plan p;
     p.units_per_wave = ups;
