@@ -281,6 +281,42 @@ def test_random_shapes_match_oracle(qmv, oracle, gpu, t, rows, cols, batch, seed
     matvec_parity(qmv, oracle, t, rows, cols, batch=batch, seed=seed, what=f"random {rows}x{cols} M={batch}")
 
 
+SWEEP_PLANS = [(0, 0, 0, 0)] * 6 + [(0, 2, 0, 0), (0, 0, 8, 0), (0, 0, 2, 0), (4096, 0, 0, 0), (0, 0, 0, 2),
+                                   (0, 1, 5, 0)]
+
+
+def test_random_sweep_with_plans(qmv, oracle, gpu):
+    """600 seeded cases in one test: any format, 1..3000 rows, K up to 29
+    super-blocks or 119 blocks, batches of 1..40, under the default plan
+    (half the cases) or a forced one (units per wave, waves per group,
+    target waves, matrix cores from two positions)."""
+    rng = np.random.default_rng(77)
+    worst = 0.0
+    for i in range(600):
+        t = B.ALL_TYPES[int(rng.integers(0, 4))]
+        rows = int(rng.choice([int(rng.integers(1, 200)), int(rng.integers(200, 3000))]))
+        cols = 256 * int(rng.integers(1, 30)) if t in (B.Q4_K, B.Q6_K) else 32 * int(rng.integers(1, 120))
+        batch = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32, 33, 40]))
+        plan = SWEEP_PLANS[int(rng.integers(0, len(SWEEP_PLANS)))]
+        raw = qmv.synth_tensor(t, rows, cols, seed=20000 + i)
+        x = qmv.synth_normal(batch * cols, seed=30000 + i).reshape(batch, cols)
+        v = qmv.make_view(raw, t, rows, cols)
+        qmv.set_launch_tuning(*plan)
+        try:
+            y = qmv.matvec(v, x if batch > 1 else x[0]).reshape(batch, rows)
+        finally:
+            qmv.set_launch_tuning(0, 0, 0, 0)
+        y_ref = oracle.matvec(raw, t, rows, cols, x if batch > 1 else x[0]).reshape(batch, rows)
+        for b in range(batch):
+            _, absdot = oracle.row_stats(raw, t, rows, cols, x[b])
+            worst = max(worst, check_rows(y[b], y_ref[b], absdot,
+                                          f"case {i}: type {t} {rows}x{cols} M={batch} plan {plan} pos {b}"))
+        qmv.release_tensor(v.data)
+        if i % 100 == 0:
+            log(f"sweep case {i}: type {t} {rows}x{cols} M={batch} plan {plan}; worst so far {worst:.2e}")
+    log(f"sweep: 600 cases, worst err/sum|wx| = {worst:.2e}")
+
+
 @pytest.mark.parametrize("t", B.ALL_TYPES)
 @pytest.mark.parametrize("batch", [1, 8, 20])
 @pytest.mark.parametrize("scale", ["1e-28", "1e28", "mixed"])
