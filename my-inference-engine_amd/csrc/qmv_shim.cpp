@@ -549,12 +549,19 @@ struct Epilogue {
  * groups: 64 us against 77 us at two); two for small launches (q|k|v, o:
  * 28 and 27 us against 41 at five), where more splits keep more CUs busy;
  * one for rows of at most 8 units in at most 8 tile groups (Q8_0 896 x 896:
- * 17.8 us against 19.3 at two for 32 positions, 11.2 against 12.8 for 16).
+ * 17.8 us against 19.3 at two for 32 positions, 11.2 against 12.8 for 16);
+ * three for long rows in at most 8 tile groups (Qwen2.5-1.5B down 1536 x
+ * 8960: 35.9 us against 38.1 at five for 32 positions, 23.3 against 26.6
+ * for 16; the 7B down, 14 groups, takes 78.6 at three against 67 at five).
  * units_per_wave, when forced, sets the units per split instead. */
 Plan plan_prefill(long long groups, int units)
 {
     const int force_u = g_force_u.load();
-    int ups = force_u > 0 ? force_u : units >= 32 || groups >= 100 ? 5 : units <= 8 && groups <= 8 ? 1 : 2;
+    int ups = force_u > 0                  ? force_u
+              : units >= 32 && groups <= 8   ? 3
+              : units >= 32 || groups >= 100 ? 5
+              : units <= 8 && groups <= 8    ? 1
+                                             : 2;
     if (ups > units) ups = units;
     Plan p;
     p.units_per_wave = ups;
