@@ -343,8 +343,9 @@ def small_configs_bench(qmv, hip, stream, reps):
     Q4_K 4864x896 gate/up shape is not a valid Q4_K tensor and is rejected,
     as by the reference) at M=1, and one Qwen2.5-1.5B layer set at M=8 (q|k|v
     Q5_0 1536/256/256x1536, o Q5_0 1536x1536, gate|up Q4_K 8960x1536, down
-    Q4_K 1536x8960) as its four launches. Cold: graph replays cycling through
-    enough copies to exceed 1 GB (twice the Infinity Cache); warm: one copy."""
+    Q4_K 1536x8960) as its four launches, also at 32 positions. Cold: graph
+    replays cycling through enough copies to exceed 1 GB (twice the Infinity
+    Cache); warm: one copy."""
     Q5_0, Q8_0 = 6, 8
     D = hip.DeviceBuffer
     sp = stream.handle
@@ -356,6 +357,9 @@ def small_configs_bench(qmv, hip, stream, reps):
                                         [("gate", Q4_K, 8960, 1536), ("up", Q4_K, 8960, 1536)],
                                         [("down", Q4_K, 1536, 8960)]]),
     }
+    # The same layer set as one prefill chunk of 32 positions (the reference
+    # prefills in chunks of 8, src/qwen2_internal.h:7).
+    cases["qwen2_1_5b_layer_set_m32"] = (32, cases["qwen2_1_5b_layer_set_m8"][1])
     out = {}
     for name, (m, groups) in cases.items():
         raws = {t[0]: qmv.synth_tensor(t[1], t[2], t[3], seed=900 + i)
