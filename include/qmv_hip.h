@@ -53,8 +53,10 @@ typedef struct QmvTensorView {
  * argument rules: input_count == dimensions[0], output_count ==
  * dimensions[1], type in {Q5_0, Q8_0, Q4_K, Q6_K}, consistent block layout.
  * The packed tensor is uploaded to HBM on first use and cached (keyed by data
- * pointer, type and shape, guarded by a sampled content fingerprint); input and
- * output are host buffers.
+ * pointer, type and shape, guarded by a content fingerprint: every byte of
+ * tensors up to 64 KiB, 64 sampled words of larger ones); input and output are
+ * host buffers. The packed bytes must not change while they are cached: after
+ * editing them in place, or before freeing them, call qmv_release_tensor.
  */
 int qmv_tensor_matvec_f32(const QmvTensorView *matrix, const float *input,
                           int input_count, float *output, int output_count);
@@ -73,11 +75,32 @@ int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs,
 #define QMV_MAX_BATCH 32
 
 /*
- * Upload a packed tensor now (at model load) instead of on first use, so
- * later matvec calls allocate nothing. No reference counterpart: the
- * reference reads weights straight from its mmap (src/gguf_reader.cpp:695-697).
+ * Upload a packed tensor now (at model load) instead of on first use. No
+ * reference counterpart: the reference reads weights straight from its mmap
+ * (src/gguf_reader.cpp:695-697). Registration alone does not size the
+ * per-thread staging or the split-K workspace; qmv_reserve_calls does.
  */
 int qmv_register_tensor(const QmvTensorView *matrix);
+
+/*
+ * Register the tensor and pre-size, for host-pointer matvec/matmul calls on
+ * it with 1..max_batch positions from the calling thread, everything those
+ * calls would otherwise allocate on first use: the thread's HIP stream, its
+ * pinned and device staging, and the stream's split-K workspace. Called for
+ * every weight from the engine's state initialisation
+ * (inference_state_init), it makes the reference's contracts hold: a forward
+ * pass allocates nothing after init (include/engine.h:84-85) and the matvec
+ * itself allocates nothing (src/quantized_matvec.h:24). A later change of the
+ * launch tuning, another thread or a larger batch may allocate again.
+ */
+int qmv_reserve_calls(const QmvTensorView *matrix, int max_batch);
+
+/*
+ * Number of device allocations, pinned host allocations and stream
+ * creations the library has made in this process (a test and diagnostic
+ * counter for the contract above).
+ */
+unsigned long long qmv_allocation_count(void);
 
 /*
  * Drop the device copies of every tensor whose host data pointer is data

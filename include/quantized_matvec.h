@@ -10,6 +10,13 @@
  * the block size, and element_count/block_count/block layout must agree with
  * the shape. Returns 1 after writing every output, 0 otherwise (output
  * contents are then unspecified).
+ *
+ * Unlike the reference, which reads the packed bytes on every call, the
+ * library keeps a device copy of each tensor it has seen, keyed by data
+ * pointer, type and shape and checked against a content fingerprint (every
+ * byte up to 64 KiB, sampled words beyond). The bytes must therefore stay
+ * unchanged while cached: after editing them in place, or before freeing or
+ * unmapping them (gguf_close), call qmv_release_tensor(data) from qmv_hip.h.
  */
 #ifndef QUANTIZED_MATVEC_H
 #define QUANTIZED_MATVEC_H

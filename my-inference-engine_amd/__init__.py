@@ -33,7 +33,7 @@ GGML_TYPE_Q6_K = 14
 BLOCK_ELEMENTS = {GGML_TYPE_Q5_0: 32, GGML_TYPE_Q8_0: 32, GGML_TYPE_Q4_K: 256, GGML_TYPE_Q6_K: 256}
 BLOCK_BYTES = {GGML_TYPE_Q5_0: 22, GGML_TYPE_Q8_0: 34, GGML_TYPE_Q4_K: 144, GGML_TYPE_Q6_K: 210}
 TYPE_NAMES = {GGML_TYPE_Q5_0: "Q5_0", GGML_TYPE_Q8_0: "Q8_0", GGML_TYPE_Q4_K: "Q4_K", GGML_TYPE_Q6_K: "Q6_K"}
-MAX_BATCH = 8
+MAX_BATCH = 32  # QMV_MAX_BATCH: positions per device call (host calls take any batch)
 MAX_GROUP = 8
 
 
@@ -84,6 +84,8 @@ HIP_SIGNATURES = {
     "qmv_tensor_matvec_f32": (ctypes.c_int, [_view_p, _vp, ctypes.c_int, _vp, ctypes.c_int]),
     "qmv_tensor_matmul_f32": (ctypes.c_int, [_view_p, _vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int]),
     "qmv_register_tensor": (ctypes.c_int, [_view_p]),
+    "qmv_reserve_calls": (ctypes.c_int, [_view_p, ctypes.c_int]),
+    "qmv_allocation_count": (ctypes.c_ulonglong, []),
     "qmv_release_tensor": (ctypes.c_int, [_vp]),
     "qmv_release_all": (None, []),
     "qmv_dequantize_rows_f32": (ctypes.c_int, [_view_p, ctypes.c_int, ctypes.c_int, _vp]),
@@ -218,6 +220,18 @@ def set_launch_tuning(target_waves: int = 0, units_per_wave: int = 0, waves_per_
 
 def register_tensor(view: QmvTensorView) -> int:
     return hip_lib().qmv_register_tensor(ctypes.byref(view))
+
+
+def reserve_calls(view: QmvTensorView, max_batch: int) -> None:
+    """Register the tensor and pre-size this thread's staging and workspace
+    for host calls of up to ``max_batch`` positions on it."""
+    if not hip_lib().qmv_reserve_calls(ctypes.byref(view), max_batch):
+        raise QmvError(last_error())
+
+
+def allocation_count() -> int:
+    """Device/pinned allocations and stream creations made by the library."""
+    return hip_lib().qmv_allocation_count()
 
 
 def release_tensor(data_ptr: int) -> int:

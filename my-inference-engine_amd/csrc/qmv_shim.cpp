@@ -79,6 +79,23 @@ bool hip_ok(hipError_t e, const char *what)
 std::atomic<int> g_device{0};
 std::atomic<int> g_fail_next{0};
 
+/* Every device, pinned-host or stream allocation the library makes, counted
+ * (qmv_allocation_count): after registration and qmv_reserve_calls, matvec
+ * calls within the reserved sizes leave it unchanged. */
+std::atomic<unsigned long long> g_allocations{0};
+
+hipError_t counted_malloc(void **p, size_t bytes)
+{
+    g_allocations.fetch_add(1);
+    return hipMalloc(p, bytes);
+}
+
+hipError_t counted_host_malloc(void **p, size_t bytes)
+{
+    g_allocations.fetch_add(1);
+    return hipHostMalloc(p, bytes, hipHostMallocDefault);
+}
+
 /* ---- validation (src/quantized_matvec.cpp:93-149, :168-191) ------------------ */
 
 struct Shape {
@@ -152,6 +169,12 @@ struct Workspace {
     uint64_t *fused_cand = nullptr;  /* fused argmax: tile and group candidates */
     unsigned *fused_count = nullptr; /* fused argmax: arrival counts, zero between launches */
     size_t fused_cap = 0;            /* tiles */
+    /* Buffers replaced by a larger one. They are never freed: a graph
+     * captured earlier on this stream still launches kernels that use them
+     * (every launch leaves its counters at zero, so such replays stay
+     * correct). Growth is geometric, so they hold less than twice the final
+     * size. */
+    std::vector<void *> retired;
     std::mutex mu;
 };
 
@@ -169,18 +192,19 @@ int workspace_reserve(Workspace &ws, hipStream_t stream, size_t partials, size_t
     HIP_TRY(hipStreamSynchronize(stream));
     if (partials > ws.partial_cap) {
         const size_t n = partials + partials / 2 + 4096;
-        if (ws.partials) HIP_TRY(hipFree(ws.partials));
-        ws.partials = nullptr;
-        ws.partial_cap = 0;
-        HIP_TRY(hipMalloc(&ws.partials, n * sizeof(float)));
+        float *np = nullptr;
+        HIP_TRY(counted_malloc((void **)&np, n * sizeof(float)));
+        if (ws.partials) ws.retired.push_back(ws.partials);
+        ws.partials = np;
         ws.partial_cap = n;
     }
     if (counters > ws.counter_cap) {
         const size_t n = counters + counters / 2 + 1024;
-        if (ws.counters) HIP_TRY(hipFree(ws.counters));
-        ws.counters = nullptr;
+        unsigned *nc = nullptr;
+        HIP_TRY(counted_malloc((void **)&nc, n * sizeof(unsigned)));
+        if (ws.counters) ws.retired.push_back(ws.counters);
+        ws.counters = nc;
         ws.counter_cap = 0;
-        HIP_TRY(hipMalloc(&ws.counters, n * sizeof(unsigned)));
         HIP_TRY(hipMemsetAsync(ws.counters, 0, n * sizeof(unsigned), stream));
         ws.counter_cap = n;
     }
@@ -201,13 +225,18 @@ int workspace_fused_argmax(Workspace &ws, hipStream_t stream, size_t tiles)
     }
     HIP_TRY(hipStreamSynchronize(stream));
     const size_t n = tiles + tiles / 2 + 256;
-    if (ws.fused_cand) HIP_TRY(hipFree(ws.fused_cand));
-    if (ws.fused_count) HIP_TRY(hipFree(ws.fused_count));
-    ws.fused_cand = nullptr;
-    ws.fused_count = nullptr;
+    uint64_t *cand = nullptr;
+    unsigned *count = nullptr;
+    HIP_TRY(counted_malloc((void **)&cand, qmv::argmax_words(n) * sizeof(uint64_t)));
+    if (!hip_ok(counted_malloc((void **)&count, qmv::argmax_counts(n) * sizeof(unsigned)), "hipMalloc")) {
+        ws.retired.push_back(cand);
+        return 0;
+    }
+    if (ws.fused_cand) ws.retired.push_back(ws.fused_cand);
+    if (ws.fused_count) ws.retired.push_back(ws.fused_count);
+    ws.fused_cand = cand;
+    ws.fused_count = count;
     ws.fused_cap = 0;
-    HIP_TRY(hipMalloc(&ws.fused_cand, qmv::argmax_words(n) * sizeof(uint64_t)));
-    HIP_TRY(hipMalloc(&ws.fused_count, qmv::argmax_counts(n) * sizeof(unsigned)));
     HIP_TRY(hipMemsetAsync(ws.fused_count, 0, qmv::argmax_counts(n) * sizeof(unsigned), stream));
     ws.fused_cap = n;
     return 1;
@@ -215,11 +244,11 @@ int workspace_fused_argmax(Workspace &ws, hipStream_t stream, size_t tiles)
 
 int workspace_argmax(Workspace &ws)
 {
-    if (ws.arg_val) return 1;
-    HIP_TRY(hipMalloc(&ws.arg_val, kArgBlocks * sizeof(float)));
-    HIP_TRY(hipMalloc(&ws.arg_idx, kArgBlocks * sizeof(int)));
-    HIP_TRY(hipMalloc(&ws.arg_bad, kArgBlocks * sizeof(int)));
-    HIP_TRY(hipMalloc(&ws.arg_result, 2 * sizeof(int)));
+    if (ws.arg_result) return 1;
+    HIP_TRY(counted_malloc((void **)&ws.arg_val, kArgBlocks * sizeof(float)));
+    HIP_TRY(counted_malloc((void **)&ws.arg_idx, kArgBlocks * sizeof(int)));
+    HIP_TRY(counted_malloc((void **)&ws.arg_bad, kArgBlocks * sizeof(int)));
+    HIP_TRY(counted_malloc((void **)&ws.arg_result, 2 * sizeof(int)));
     return 1;
 }
 
@@ -279,6 +308,7 @@ HostCtx *host_ctx()
     if (c->device != dev) {
         /* Fresh device: new stream and buffers (old ones stay with the old device). */
         *c = HostCtx();
+        g_allocations.fetch_add(1);
         if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
         c->device = dev;
     }
@@ -292,7 +322,7 @@ int grow_pinned(float **p, size_t *cap, size_t n)
     *p = nullptr;
     *cap = 0;
     const size_t m = n + n / 2 + 1024;
-    HIP_TRY(hipHostMalloc((void **)p, m * sizeof(float), hipHostMallocDefault));
+    HIP_TRY(counted_host_malloc((void **)p, m * sizeof(float)));
     *cap = m;
     return 1;
 }
@@ -304,7 +334,7 @@ int grow_device(float **p, size_t *cap, size_t n)
     *p = nullptr;
     *cap = 0;
     const size_t m = n + n / 2 + 1024;
-    HIP_TRY(hipMalloc((void **)p, m * sizeof(float)));
+    HIP_TRY(counted_malloc((void **)p, m * sizeof(float)));
     *cap = m;
     return 1;
 }
@@ -344,10 +374,10 @@ int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_
     t->data = nullptr;
 
     uint8_t *raw = nullptr;
-    HIP_TRY(hipMalloc(&raw, t->packed_bytes));
+    HIP_TRY(counted_malloc((void **)&raw, t->packed_bytes));
     std::unique_ptr<uint8_t, hipError_t (*)(void *)> raw_guard(raw, hipFree);
     HIP_TRY(hipMemcpyAsync(raw, m->data, t->packed_bytes, hipMemcpyHostToDevice, stream));
-    HIP_TRY(hipMalloc(&t->data, t->device_bytes));
+    HIP_TRY(counted_malloc((void **)&t->data, t->device_bytes));
     if (t->device_bytes != t->packed_bytes) HIP_TRY(hipMemsetAsync(t->data, 0, t->device_bytes, stream));
     HIP_TRY(qmv::launch_repack(s.geo.format, raw, t->data, s.rows, s.blocks_per_row, t->units,
                                s.geo.blocks_per_unit, s.geo.block_bytes, s.geo.unit_bytes, t->tiles, stream));
@@ -356,11 +386,26 @@ int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_
     return 1;
 }
 
-/* Sampled fingerprint of the host bytes: catches a reused data pointer that
- * now holds a different tensor (the reference's views die at gguf_close). */
+/* Fingerprint of the host bytes: catches a reused data pointer that now
+ * holds a different tensor (the reference's views die at gguf_close). Every
+ * byte of tensors up to kFullHashBytes (a few microseconds of hashing), 64
+ * sampled words of larger ones, whose callers release them on change. */
+constexpr uint64_t kFullHashBytes = 64u << 10;
+
 uint64_t fingerprint(const QmvTensorView *m, uint64_t bytes)
 {
     uint64_t h = 0x9E3779B97F4A7C15ull ^ bytes;
+    if (bytes <= kFullHashBytes) {
+        uint64_t off = 0;
+        for (; off + 8 <= bytes; off += 8) {
+            uint64_t w;
+            memcpy(&w, m->data + off, 8);
+            h = (h ^ w) * 0x100000001b3ull;
+            h ^= h >> 29;
+        }
+        for (; off < bytes; ++off) h = (h ^ m->data[off]) * 0x100000001b3ull;
+        return h;
+    }
     const int samples = 64;
     for (int i = 0; i < samples; ++i) {
         uint64_t off = bytes <= 8 ? 0 : (bytes - 8) * (uint64_t)i / (uint64_t)(samples - 1);
@@ -571,11 +616,23 @@ Plan plan_prefill(long long groups, int units)
     return p;
 }
 
-/* Enqueue one launch over `count` tensors sharing the input, for positions
+/* One launch over `count` tensors sharing the input, for positions
  * [b0, b0 + batch) of the caller's batch (the caller's pointers are offset
- * here). */
-int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, int batch,
-                 float *const *d_out, hipStream_t stream, Workspace &ws, const Epilogue &epi)
+ * here), planned but not enqueued: the parameters, the grid and the workspace
+ * it needs. The workspace pointers are filled in by whoever owns the memory
+ * (a per-stream workspace, or the fixed device scratch of the no-allocation
+ * entry point). */
+struct ChunkPlan {
+    qmv::MatvecParams p;
+    bool prefill = false, paired = false;
+    int mt = 1, grid = 0, waves = 0, fmt = 0;
+    size_t partials = 0, counters = 0;     /* floats / words of split-K workspace */
+    size_t pair_vals = 0, pair_count = 0;  /* offsets of the SwiGLU tile-pair region */
+    size_t argmax_tiles = 0;               /* fused argmax candidate slots needed (0: none) */
+};
+
+int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, int batch, float *const *d_out,
+               const Epilogue &epi, ChunkPlan *cp)
 {
     const QmvDeviceTensor *t0 = ts[0];
     const bool mfma = use_matrix_cores(t0->geo.format, batch);
@@ -609,7 +666,7 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
                                          mfma || parts > 1 ? 1 : 8);
 
-    qmv::MatvecParams p;
+    qmv::MatvecParams &p = cp->p;
     memset(&p, 0, sizeof p);
     p.njobs = count;
     p.x = d_in + (size_t)b0 * t0->cols;
@@ -666,7 +723,8 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (paired) p.pair_waves = plan.waves;
     /* Fused SwiGLU otherwise: both projections' final tiles, then one count
      * per tile pair, after the split-K partials and counters. */
-    const size_t pair_vals = partials, pair_count = counters;
+    cp->pair_vals = partials;
+    cp->pair_count = counters;
     if (epi.swiglu && !paired) {
         if (count != 2 || ts[0]->rows != ts[1]->rows) {
             set_error("fused SwiGLU takes two tensors (gate, up) with equal rows");
@@ -681,48 +739,93 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         return 0;
     }
     p.matrix_cores = mfma;
-    std::lock_guard<std::mutex> lock(ws.mu);
-    if (!workspace_reserve(ws, stream, partials, counters)) return 0;
-    p.partials = ws.partials;
-    p.counters = ws.counters;
-    if (epi.swiglu && !paired) {
-        p.pair_vals = ws.partials + pair_vals;
-        p.pair_count = ws.counters + pair_count;
-    }
+    cp->argmax_tiles = 0;
     if (epi.argmax) {
         if (count != 1 || batch != 1 || b0 != 0 || epi.swiglu) {
             set_error("fused argmax takes one tensor and one position");
             return 0;
         }
-        if (!workspace_fused_argmax(ws, stream, (size_t)t0->tiles)) return 0;
-        p.argmax_cand = ws.fused_cand;
-        p.argmax_count = ws.fused_count;
         p.argmax_result = epi.argmax;
         p.argmax_tiles = t0->tiles;
+        cp->argmax_tiles = (size_t)t0->tiles;
     }
-    if (prefill)
-        HIP_TRY(qmv::launch_prefill(t0->geo.format, p, mt, (int)wg, stream));
-    else
-        HIP_TRY(qmv::launch_matvec(t0->geo.format, p, mt, (int)wg, paired ? 2 * plan.waves : plan.waves, stream));
+    cp->prefill = prefill;
+    cp->paired = paired;
+    cp->mt = mt;
+    cp->grid = (int)wg;
+    cp->waves = paired ? 2 * plan.waves : plan.waves;
+    cp->fmt = t0->geo.format;
+    cp->partials = partials;
+    cp->counters = counters;
     return 1;
 }
 
-/* Positions per launch for a batch: up to 32 on the matrix cores (Q4_K and
- * Q6_K prefill), else 8. */
+/* Point the plan at its split-K workspace: partials[cp.partials] floats and
+ * counters[cp.counters] words (zero between launches). */
+void bind_workspace(ChunkPlan &cp, float *partials, unsigned *counters)
+{
+    cp.p.partials = partials;
+    cp.p.counters = counters;
+    if (cp.p.swiglu) {
+        cp.p.pair_vals = partials + cp.pair_vals;
+        cp.p.pair_count = counters + cp.pair_count;
+    }
+}
+
+int enqueue_chunk(const ChunkPlan &cp, hipStream_t stream)
+{
+    if (cp.prefill)
+        HIP_TRY(qmv::launch_prefill(cp.fmt, cp.p, cp.mt, cp.grid, stream));
+    else
+        HIP_TRY(qmv::launch_matvec(cp.fmt, cp.p, cp.mt, cp.grid, cp.waves, stream));
+    return 1;
+}
+
+/* Plan a launch and enqueue it on the stream's own workspace (grown here if
+ * needed, outside graph capture only). */
+int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, int batch,
+                 float *const *d_out, hipStream_t stream, Workspace &ws, const Epilogue &epi)
+{
+    ChunkPlan cp;
+    if (!plan_chunk(ts, count, d_in, b0, batch, d_out, epi, &cp)) return 0;
+    std::lock_guard<std::mutex> lock(ws.mu);
+    if (!workspace_reserve(ws, stream, cp.partials, cp.counters)) return 0;
+    bind_workspace(cp, ws.partials, ws.counters);
+    if (cp.argmax_tiles) {
+        if (!workspace_fused_argmax(ws, stream, cp.argmax_tiles)) return 0;
+        cp.p.argmax_cand = ws.fused_cand;
+        cp.p.argmax_count = ws.fused_count;
+    }
+    return enqueue_chunk(cp, stream);
+}
+
+/* Positions per launch for the remaining `batch` positions of a call: up to
+ * 32 where the prefill kernel takes them, else 8. */
 int chunk_positions(int fmt, int batch)
 {
     const int wide = batch < QMV_MFMA_MAX_POSITIONS ? batch : QMV_MFMA_MAX_POSITIONS;
     return use_prefill(fmt, wide) ? QMV_MFMA_MAX_POSITIONS : QMV_VALU_MAX_POSITIONS;
 }
 
+/* Positions of the launch that starts at position b0 of a `batch`-position
+ * call. The chunk size is chosen again for every launch from the positions
+ * left, so a tail that the prefill kernel does not take (for instance below
+ * a raised matrix-core threshold) runs in launches of at most 8. */
+int next_chunk(int fmt, int batch, int b0)
+{
+    const int left = batch - b0;
+    const int chunk = chunk_positions(fmt, left);
+    return left < chunk ? left : chunk;
+}
+
 /* Enqueue a batch of any size as launches of up to chunk_positions(). */
 int launch_group(QmvDeviceTensor *const *ts, int count, const float *d_in, int batch, float *const *d_out,
                  hipStream_t stream, Workspace &ws, const Epilogue &epi = Epilogue())
 {
-    const int chunk = chunk_positions(ts[0]->geo.format, batch);
-    for (int b0 = 0; b0 < batch; b0 += chunk) {
-        const int nb = batch - b0 < chunk ? batch - b0 : chunk;
+    for (int b0 = 0; b0 < batch;) {
+        const int nb = next_chunk(ts[0]->geo.format, batch, b0);
         if (!launch_chunk(ts, count, d_in, b0, nb, d_out, stream, ws, epi)) return 0;
+        b0 += nb;
     }
     return 1;
 }
@@ -792,6 +895,50 @@ QMV_API int qmv_register_tensor(const QmvTensorView *matrix)
     HostCtx *c = host_ctx();
     if (!c) return 0;
     return cached_tensor(matrix, s, c) ? 1 : 0;
+}
+
+/* Pre-size everything a host-pointer call on this tensor needs, for batches
+ * of 1..max_batch positions: the upload, the calling thread's stream and
+ * staging, and its stream's split-K workspace for every launch such a call
+ * makes (launches carry at most QMV_MFMA_MAX_POSITIONS positions, and a
+ * launch's needs depend only on its own position count). */
+QMV_API int qmv_reserve_calls(const QmvTensorView *matrix, int max_batch)
+{
+    Shape s;
+    if (!view_layout_ok(matrix, &s)) return 0;
+    if (max_batch <= 0 || (size_t)max_batch > SIZE_MAX / 4 / (size_t)(s.cols > s.rows ? s.cols : s.rows)) {
+        set_error("max_batch must be positive and its staging addressable");
+        return 0;
+    }
+    HostCtx *c = host_ctx();
+    if (!c) return 0;
+    std::shared_ptr<QmvDeviceTensor> t = cached_tensor(matrix, s, c);
+    if (!t) return 0;
+    const size_t nin = (size_t)max_batch * (size_t)s.cols, nout = (size_t)max_batch * (size_t)s.rows;
+    if (!grow_pinned(&c->h_in, &c->h_in_cap, nin) || !grow_pinned(&c->h_out, &c->h_out_cap, nout) ||
+        !grow_device(&c->d_in, &c->d_in_cap, nin))
+        return 0;
+    QmvDeviceTensor *tp = t.get();
+    float *out = c->d_in; /* planning only: no launch is made */
+    size_t need_p = 0, need_c = 0;
+    const int widest = max_batch < QMV_MFMA_MAX_POSITIONS ? max_batch : QMV_MFMA_MAX_POSITIONS;
+    for (int nb = 1; nb <= widest; ++nb) {
+        if (nb > QMV_VALU_MAX_POSITIONS && !use_prefill(tp->geo.format, nb)) continue;
+        ChunkPlan cp;
+        if (!plan_chunk(&tp, 1, c->d_in, 0, nb, &out, Epilogue(), &cp)) return 0;
+        if (cp.partials > need_p) need_p = cp.partials;
+        if (cp.counters > need_c) need_c = cp.counters;
+    }
+    Workspace &ws = workspace_for(c->device, c->stream);
+    std::lock_guard<std::mutex> lock(ws.mu);
+    if (!workspace_reserve(ws, c->stream, need_p, need_c)) return 0;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return 1;
+}
+
+QMV_API unsigned long long qmv_allocation_count(void)
+{
+    return g_allocations.load();
 }
 
 QMV_API int qmv_release_tensor(const unsigned char *data)

@@ -87,6 +87,9 @@ class DeviceBuffer:
 
 
 class Stream:
+    """A HIP stream (default priority), destroyed by destroy() or on leaving a
+    ``with`` block after its work has finished."""
+
     def __init__(self):
         s = ctypes.c_void_p()
         check(rt().hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
@@ -94,6 +97,18 @@ class Stream:
 
     def synchronize(self) -> None:
         check(rt().hipStreamSynchronize(self.handle), "hipStreamSynchronize")
+
+    def destroy(self) -> None:
+        if self.handle:
+            rt().hipStreamSynchronize(self.handle)
+            rt().hipStreamDestroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
 
 
 class Event:
@@ -111,11 +126,15 @@ class Event:
         return ms.value
 
     def destroy(self) -> None:
-        rt().hipEventDestroy(self.handle)
+        if self.handle:
+            rt().hipEventDestroy(self.handle)
+            self.handle = None
 
 
 class Graph:
-    """Captures everything enqueued on `stream` between begin() and end()."""
+    """Captures everything enqueued on `stream` between begin() and end();
+    destroy() (or leaving a ``with`` block) frees the executable graph and the
+    graph after the stream's work has finished."""
 
     def __init__(self, stream: Stream):
         self.stream = stream
@@ -135,6 +154,22 @@ class Graph:
 
     def replay(self) -> None:
         check(rt().hipGraphLaunch(self.exec, self.stream.handle), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if self.stream.handle:
+            rt().hipStreamSynchronize(self.stream.handle)
+        if self.exec:
+            rt().hipGraphExecDestroy(self.exec)
+            self.exec = None
+        if self.graph:
+            rt().hipGraphDestroy(self.graph)
+            self.graph = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
 
 
 def synchronize() -> None:

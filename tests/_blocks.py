@@ -22,6 +22,7 @@ Q5_0, Q8_0, Q4_K, Q6_K = 6, 8, 12, 14
 BLOCK_ELEMENTS = {Q5_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
 BLOCK_BYTES = {Q5_0: 22, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 ALL_TYPES = (Q5_0, Q8_0, Q4_K, Q6_K)
+NAMES = {Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 KATS = json.load(open(os.path.join(HERE, "golden", "reference_kats.json")))
