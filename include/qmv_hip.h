@@ -166,6 +166,32 @@ int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int count,
                                 float *const *d_outputs, void *stream);
 
 /*
+ * qmv_device_matvec_group_f32 without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The split-K workspace is a fixed array in device memory of
+ * QMV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends: arrival
+ * counters in its first QMV_NOALLOC_COUNTER_BYTES (one 128-byte line per
+ * tile whose K is split, so at most 4096 such tiles per launch) and partial
+ * sums in the rest (31.5 MiB, 8,257,536 floats). A call whose
+ * launches would need more is rejected (return 0, nothing launched); the
+ * decode and prefill shapes of a 7B model fit (for example a 151936 x 3584
+ * vocabulary projection for one position: 455,808 floats, or one 18944 x
+ * 3584 projection for 32 positions: 4,243,456 floats); the vocabulary
+ * projection for 8 positions (8.5 M floats) does not. The
+ * counters are cleared by a fill kernel before each launch (no memset node).
+ * All calls on one GPU share its array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must be serialised by the
+ * caller. Results are bit-identical to qmv_device_matvec_group_f32.
+ */
+#define QMV_NOALLOC_SCRATCH_BYTES (32u << 20)
+#define QMV_NOALLOC_COUNTER_BYTES (512u << 10)
+int qmv_device_matvec_group_noalloc_f32(const qmv_device_tensor *tensors,
+                                        int count, const float *d_inputs,
+                                        int batch_count,
+                                        float *const *d_outputs, void *stream);
+
+/*
  * Grouped matvec with an addend fused into the store: for each tensor i,
  * d_outputs[i][b*N_i + r] = (W_i x_b)[r] + d_addends[i][b*addend_strides[i] + r]
  * (the fp32 sum of the row result and the addend, as the reference's separate

@@ -98,6 +98,8 @@ HIP_SIGNATURES = {
     "qmv_device_matvec_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
     "qmv_device_matvec_group_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, ctypes.c_int,
                                                    ctypes.POINTER(_vp), _vp]),
+    "qmv_device_matvec_group_noalloc_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, ctypes.c_int,
+                                                           ctypes.POINTER(_vp), _vp]),
     "qmv_device_dequantize_f32": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "qmv_device_greedy_argmax_f32": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp]),
     "qmv_last_error": (ctypes.c_char_p, []),
@@ -285,6 +287,17 @@ def device_matvec_group(tensors: Sequence[DeviceTensor], d_x: int, batch: int, d
     hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
     outs = (ctypes.c_void_p * n)(*d_outs)
     if not hip_lib().qmv_device_matvec_group_f32(hs, n, d_x, batch, outs, stream):
+        raise QmvError(last_error())
+
+
+def device_matvec_group_noalloc(tensors: Sequence[DeviceTensor], d_x: int, batch: int, d_outs: Sequence[int],
+                                stream: int = 0) -> None:
+    """device_matvec_group with its split-K workspace in the library's fixed
+    device scratch array: allocates nothing; overlapping calls on one GPU race."""
+    n = len(tensors)
+    hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
+    outs = (ctypes.c_void_p * n)(*d_outs)
+    if not hip_lib().qmv_device_matvec_group_noalloc_f32(hs, n, d_x, batch, outs, stream):
         raise QmvError(last_error())
 
 

@@ -98,6 +98,8 @@ hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, in
 hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s);
 /* Plain fp32 copy (n elements) as a kernel, e.g. from mapped host memory. */
 hipError_t launch_copy(const float *src, float *dst, size_t n, hipStream_t s);
+/* dst[0..n) = v (a fill kernel, no memset node). */
+hipError_t launch_fill_u32(unsigned *dst, size_t n, unsigned v, hipStream_t s);
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out,
                            hipStream_t s);
 hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int *bbad, int nblocks,

@@ -2641,6 +2641,22 @@ hipError_t launch_copy(const float *src, float *dst, size_t n, hipStream_t s)
     return hipGetLastError();
 }
 
+/* dst[0..n) = v with vector stores: clears counters where a memset node
+ * must not be used (code a caller may capture into a graph). */
+__global__ void __launch_bounds__(256) fill_u32_kernel(unsigned *__restrict__ dst, size_t n, unsigned v)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = v;
+}
+
+hipError_t launch_fill_u32(unsigned *dst, size_t n, unsigned v, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_rms_norm(const float *x, const float *w, int n, int batch, float eps, float *out, hipStream_t s)
 {
     hipLaunchKernelGGL(rms_norm_kernel, dim3(batch), dim3(QMV_NORM_THREADS), 0, s, x, w, n, eps, out);

@@ -1146,6 +1146,88 @@ QMV_API int qmv_device_matvec_group_f32(const qmv_device_tensor *tensors, int co
                         ws);
 }
 
+/* ---- no-allocation grouped matvec ----------------------------------------------
+ * The split-K workspace of these launches is a fixed device array: counters
+ * in its first QMV_NOALLOC_COUNTER_BYTES, partials in the rest. In host code
+ * the name `scratch` is only a stand-in for the array; its device address
+ * comes from hipGetSymbolAddress, once per device with that device current,
+ * and only that address is passed to kernels. Every call on a device shares
+ * its array: calls that overlap on one device race. */
+static __device__ __align__(256) unsigned char scratch[QMV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices];
+
+/* Device address of this device's scratch array (the device is current). */
+int scratch_address(int device, void **out)
+{
+    if (device < 0 || device >= kScratchDevices) {
+        set_error("device %d out of range for the no-allocation scratch", device);
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void *p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) {
+            set_error("hipGetSymbolAddress returned no address for the scratch array");
+            return 0;
+        }
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return 1;
+}
+
+} // namespace
+
+QMV_API int qmv_device_matvec_group_noalloc_f32(const qmv_device_tensor *tensors, int count, const float *d_inputs,
+                                                int batch_count, float *const *d_outputs, void *stream)
+{
+    if (!group_args_ok(tensors, count, d_inputs, batch_count, d_outputs)) return 0;
+    const int dev = tensors[0]->device;
+    HIP_TRY(hipSetDevice(dev));
+    void *base = nullptr;
+    if (!scratch_address(dev, &base)) return 0;
+    unsigned *counters = (unsigned *)base;
+    float *partials = (float *)((unsigned char *)base + QMV_NOALLOC_COUNTER_BYTES);
+    const size_t counter_cap = QMV_NOALLOC_COUNTER_BYTES / sizeof(unsigned);
+    const size_t partial_cap = (QMV_NOALLOC_SCRATCH_BYTES - QMV_NOALLOC_COUNTER_BYTES) / sizeof(float);
+    QmvDeviceTensor *const *ts = const_cast<QmvDeviceTensor *const *>(tensors);
+    const int fmt = ts[0]->geo.format;
+    /* Every launch is planned and checked before the first is enqueued, so a
+     * call that does not fit launches nothing. */
+    for (int b0 = 0; b0 < batch_count;) {
+        const int nb = next_chunk(fmt, batch_count, b0);
+        ChunkPlan cp;
+        if (!plan_chunk(ts, count, d_inputs, b0, nb, d_outputs, Epilogue(), &cp)) return 0;
+        if (cp.partials > partial_cap || cp.counters > counter_cap) {
+            set_error("launch needs %zu partial floats and %zu counters; the no-allocation scratch holds %zu and "
+                      "%zu (use qmv_device_matvec_group_f32)",
+                      cp.partials, cp.counters, partial_cap, counter_cap);
+            return 0;
+        }
+        b0 += nb;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    for (int b0 = 0; b0 < batch_count;) {
+        const int nb = next_chunk(fmt, batch_count, b0);
+        ChunkPlan cp;
+        if (!plan_chunk(ts, count, d_inputs, b0, nb, d_outputs, Epilogue(), &cp)) return 0;
+        bind_workspace(cp, partials, counters);
+        /* The counters must be zero when the launch starts. Completed
+         * launches leave them zero; the fill (a kernel, not a memset node, so
+         * the call can be captured) also covers an interrupted earlier one. */
+        HIP_TRY(qmv::launch_fill_u32(counters, cp.counters, 0u, s));
+        if (!enqueue_chunk(cp, s)) return 0;
+        b0 += nb;
+    }
+    return 1;
+}
+
 QMV_API int qmv_device_matvec_f32(qmv_device_tensor tensor, const float *d_inputs, int batch_count,
                                   float *d_outputs, void *stream)
 {
