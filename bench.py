@@ -39,6 +39,23 @@ sys.path.insert(0, ROOT)
 
 METRIC = "weight-stream GB/s and % of HBM peak; µs per decode-step matvec set (1 GPU)"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X vector fp32 (the reference's arithmetic: fp32 FMA)
+
+
+def batch_roofline(weight_bytes, flops, seconds):
+    """Both bounds of a configuration: packed weight bytes over the HBM peak
+    and the product's fp32 arithmetic (2 x positions x rows x columns flops)
+    over the fp32 vector peak; `bound` names the larger fraction. The
+    matrix-core and prefill paths compute the same exact products from three
+    bf16 limbs per activation, so this fp32 figure is the algorithmic rate,
+    not the matrix-core issue rate."""
+    gbs = weight_bytes / seconds / 1e9
+    tflops = flops / seconds / 1e12
+    hbm, fp32 = gbs / HBM_PEAK_GBS, tflops / FP32_PEAK_TFLOPS
+    return {"bound": "hbm" if hbm >= fp32 else "fp32", "frac": round(max(hbm, fp32), 4),
+            "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(hbm, 4)},
+            "fp32": {"achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(fp32, 4)}}
 LAYERS, HIDDEN, INTER, KV = 28, 3584, 18944, 512
 Q4_K, Q6_K = 12, 14
 
@@ -74,9 +91,50 @@ def _time_cpu(fn, views, xs, ys, batch, seconds):
     return statistics.median(times), len(times)
 
 
+_HOST_CPUS = None
+
+
+def host_cpus():
+    """CPUs this process may run on, the physical cores among them (distinct
+    package/core pairs) and the CPU model name, from the kernel's view. Taken
+    once, before the OpenMP runtime binds the main thread to one place
+    (OMP_PROC_BIND), after which the thread's own affinity is that place."""
+    global _HOST_CPUS
+    if _HOST_CPUS is not None:
+        return _HOST_CPUS
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    _HOST_CPUS = (len(cpus), len(cores), model)
+    return _HOST_CPUS
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: OMP_NUM_THREADS where the environment
+    sets it (the GPU box's CPU share), else every physical core this process
+    may use."""
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return env if env > 0 else host_cpus()[1]
+
+
 def cpu_baseline(qmv, host_layer, batch, seconds):
     """Time the reference's CPU path (its own sources, x86 Release flags with
-    AVX2/FMA/F16C and OpenMP) on layer 0's seven matvecs for ~`seconds`."""
+    AVX2/FMA/F16C and OpenMP) on layer 0's seven matvecs for ~`seconds`, with
+    the thread count applied to the OpenMP runtime that runs it and read back
+    from it."""
     import oracle
 
     kind = "reference"
@@ -84,14 +142,21 @@ def cpu_baseline(qmv, host_layer, batch, seconds):
     if lib is None:
         kind, lib = "port", oracle.lib()
     fn = lib.ref_quantized_tensor_matmul_f32 if kind == "reference" else lib.oracle_matmul_f32
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    gomp = ctypes.CDLL("libgomp.so.1")  # the runtime the library already loaded
+    threads = cpu_threads()
+    gomp.omp_set_num_threads(threads)
+    applied = gomp.omp_get_max_threads()
     views, xs, ys, nbytes = _cpu_layer(qmv, host_layer, batch)
     med, reps = _time_cpu(fn, views, xs, ys, batch, seconds)
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+    ncpu, ncores, model = host_cpus()
+    env = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")}
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": applied, "kind": kind,
             "sample": f"layer 0 of the set (7 matvecs, {nbytes} packed bytes, M={batch}), "
                       f"{reps} repetitions, median {med * 1e3:.1f} ms "
                       f"({'oracle/_ref/libref_avx2.so: -O3 -mavx2 -mfma -mf16c -fopenmp' if kind == 'reference' else 'oracle/liboracle.so scalar port'}, "
-                      f"OMP_NUM_THREADS={threads})"}
+                      f"omp_get_max_threads()={applied})",
+            "host": {"nproc": ncpu, "physical_cores": ncores, "cpu_model": model,
+                     "omp_get_max_threads": applied, "env": env}}
 
 
 def cpu_variants(qmv, host_layer, batch, seconds):
@@ -196,6 +261,10 @@ def run_set(qmv, hip, stream, launches, steps, warmup, use_graph):
             step()
         stream.synchronize()
         eager = (time.perf_counter() - t0) / reps
+    for m in marks:
+        m.destroy()
+    if graph is not None:
+        graph.destroy()
     q = lambda f: per_step[min(len(per_step) - 1, int(f * len(per_step)))]
     return {"elapsed": elapsed, "ms_per_step": elapsed / steps * 1e3, "p10": q(0.1), "p50": q(0.5),
             "p90": q(0.9), "eager_ms": eager * 1e3 if eager else None, "graph": graph is not None}
@@ -229,6 +298,10 @@ def launch_profile(hip, stream, launches, passes, use_graph):
         e1.record(stream)
         stream.synchronize()
         per_kernel[name] = [passes * sum(b for b, _ in mine), e0.elapsed_ms(e1), passes * len(mine)]
+        e0.destroy()
+        e1.destroy()
+        if graph is not None:
+            graph.destroy()
     return per_kernel
 
 
@@ -269,6 +342,9 @@ def vocab_bench(qmv, hip, stream, reps):
         stream.synchronize()
         us = e0.elapsed_ms(e1) / reps * 1e3
         out[name + "_us"] = round(us, 2)
+        e0.destroy()
+        e1.destroy()
+        g.destroy()
     out["matvec_gbs"] = round(nbytes / (out["matvec_us"] * 1e-6) / 1e9, 1)
     dt.close()
     return out
@@ -293,7 +369,11 @@ def graph_us(hip, stream, fns, reps):
         g.replay()
     e1.record(stream)
     stream.synchronize()
-    return e0.elapsed_ms(e1) / reps * 1e3
+    us = e0.elapsed_ms(e1) / reps * 1e3
+    e0.destroy()
+    e1.destroy()
+    g.destroy()
+    return us
 
 
 def decode_ops_bench(qmv, hip, stream, layers, reps):
@@ -365,6 +445,7 @@ def small_configs_bench(qmv, hip, stream, reps):
         raws = {t[0]: qmv.synth_tensor(t[1], t[2], t[3], seed=900 + i)
                 for i, t in enumerate(x for g in groups for x in g)}
         nbytes = sum(r.size for r in raws.values())
+        flops = 2 * m * sum(t[2] * t[3] for g in groups for t in g)
         copies = max(2, -(-(1 << 30) // nbytes))
         sets = [{t[0]: qmv.DeviceTensor(qmv.make_view(raws[t[0]], t[1], t[2], t[3])) for g in groups for t in g}
                 for _ in range(copies)]
@@ -381,7 +462,8 @@ def small_configs_bench(qmv, hip, stream, reps):
         warm = graph_us(hip, stream, launches(sets[0]) * copies, reps) / copies
         out[name] = {"packed_bytes": nbytes, "launches": len(groups), "positions": m, "copies_cold": copies,
                      "cold_us": round(cold, 2), "warm_us": round(warm, 2),
-                     "cold_weight_gbs": round(nbytes / (cold * 1e-6) / 1e9, 1)}
+                     "cold_weight_gbs": round(nbytes / (cold * 1e-6) / 1e9, 1),
+                     "roofline_cold": batch_roofline(nbytes, flops, cold * 1e-6)}
         for ts in sets:
             for d in ts.values():
                 d.close()
@@ -415,6 +497,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the M=8 set and the read probe")
     args = ap.parse_args()
+    # Thread placement for the CPU baseline, set before any library starts
+    # the OpenMP runtime (it reads these once).
+    host_cpus()
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this path has no multi-GPU mode); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -461,6 +548,7 @@ def main():
         outs.append(o)
     hip.synchronize()
 
+    set_weights = LAYERS * sum(rows * cols for _, _, rows, cols in layer_shapes())  # rows x columns
     launches = build_launches(lib, layers, acts, outs, M)
     main_run = run_set(qmv, hip, stream, launches, args.steps, args.warmup, not args.no_graph)
     passes = max(1, args.profile_passes)
@@ -488,7 +576,9 @@ def main():
             extra[f"m{mb}_set"] = {"ms_per_step": round(rb["ms_per_step"], 4),
                                    "weight_gbs": round(total_bytes / (rb["elapsed"] / max(5, args.steps // 5)) / 1e9,
                                                        1),
-                                   "positions_per_s": round(mb / (rb["ms_per_step"] * 1e-3), 1)}
+                                   "positions_per_s": round(mb / (rb["ms_per_step"] * 1e-3), 1),
+                                   "roofline": batch_roofline(total_bytes, 2 * mb * set_weights,
+                                                              rb["ms_per_step"] * 1e-3)}
         extra["vocab_projection"] = vocab_bench(qmv, hip, stream, max(10, args.steps // 2))
         if M == 1:
             ops = decode_ops_bench(qmv, hip, stream, layers, max(10, args.steps // 2))

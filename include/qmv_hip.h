@@ -238,11 +238,15 @@ int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *d_input,
  * to fp32 (i < count <= 65535), bit-identical to the reference's per-row
  * decode qwen2_decode_quantized_embedding_row (src/qwen2_architecture.cpp:
  * 375-456) for each id. The ids are read on the device (for example the token
- * just written by qmv_device_matvec_argmax_f32); an id outside [0, N) cannot
- * be rejected there and fills its output row with NaN instead.
+ * just written by qmv_device_matvec_argmax_f32), so an id outside [0, N)
+ * cannot be rejected before the launch: its output row is filled with NaN,
+ * and if d_status is not NULL, d_status[0] is set to 1 when every id was in
+ * range and to 0 otherwise, so the caller can fail the step as the reference
+ * does for an out-of-range token (src/qwen2_architecture.cpp:384-393).
  */
 int qmv_device_embed_rows_f32(qmv_device_tensor tensor, const int *d_token_ids,
-                              int count, float *d_output, void *stream);
+                              int count, float *d_output, int *d_status,
+                              void *stream);
 
 /* Device decode of rows into d_output[row_count, K] (see qmv_dequantize_rows_f32). */
 int qmv_device_dequantize_f32(qmv_device_tensor tensor, int first_row,

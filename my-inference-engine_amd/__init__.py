@@ -107,7 +107,7 @@ HIP_SIGNATURES = {
     "qmv_device_count": (ctypes.c_int, []),
     "qmv_debug_fail_next_calls": (None, [ctypes.c_int]),
     "qmv_device_matvec_argmax_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
-    "qmv_device_embed_rows_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp]),
+    "qmv_device_embed_rows_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]),
     "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qmv_device_matvec_add_group_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, ctypes.c_int,
                                                        ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int),
@@ -334,9 +334,11 @@ def device_matvec_argmax(tensor: "DeviceTensor", d_x: int, d_logits: int, d_resu
         raise QmvError(last_error())
 
 
-def device_embed_rows(tensor: "DeviceTensor", d_ids: int, count: int, d_out: int, stream: int = 0) -> None:
-    """Decode rows d_ids[0..count) of a device tensor into d_out[count, K]."""
-    if hip_lib().qmv_device_embed_rows_f32(tensor.handle, d_ids, count, d_out, stream) != 1:
+def device_embed_rows(tensor: "DeviceTensor", d_ids: int, count: int, d_out: int, stream: int = 0,
+                      d_status: int = 0) -> None:
+    """Decode rows d_ids[0..count) of a device tensor into d_out[count, K];
+    with d_status, d_status[0] = 1 if every id was in range, else 0."""
+    if hip_lib().qmv_device_embed_rows_f32(tensor.handle, d_ids, count, d_out, d_status or None, stream) != 1:
         raise QmvError(last_error())
 
 

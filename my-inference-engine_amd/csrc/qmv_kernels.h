@@ -88,8 +88,9 @@ inline size_t argmax_counts(size_t tiles) { return (tiles + 63) / 64 + 1; }
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
+/* status (may be null): cleared to 0 if any id is outside [0, rows). */
 hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, float *out, int rows, int cols,
-                         int units, hipStream_t s);
+                         int units, int *status, hipStream_t s);
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
                          int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
                          hipStream_t s);

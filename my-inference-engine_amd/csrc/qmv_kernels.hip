@@ -2308,11 +2308,13 @@ dequant_kernel(const uint8_t *__restrict__ w, float *__restrict__ out, int rows,
  * dequant_kernel (bit-identical to the block decoders). One lane per
  * (position i, K-unit); the row's bytes of a unit sit at lane id % 64 of its
  * slab. An id outside [0, rows) fills its output row with NaN (ids live in
- * device memory, so the host cannot check them). */
+ * device memory, so the host cannot check them) and, when status is given
+ * (set to 1 beforehand), clears status[0], so the caller can fail as the
+ * reference does for such a token. */
 template <int FMT>
 __global__ void __launch_bounds__(64)
 gather_rows_kernel(const uint8_t *__restrict__ w, const int *__restrict__ ids, float *__restrict__ out, int rows,
-                   int cols, int units)
+                   int cols, int units, int *__restrict__ status)
 {
     using Unit = typename UnitOf<FMT>::T;
     constexpr int SLAB = UnitOf<FMT>::kBytes * 64;
@@ -2325,6 +2327,7 @@ gather_rows_kernel(const uint8_t *__restrict__ w, const int *__restrict__ ids, f
     const int kleft = cols - unit * UW;
     if (id < 0 || id >= rows) {
         for (int k = 0; k < UW && k < kleft; ++k) dst[k] = __builtin_nanf("");
+        if (status != nullptr && unit == 0) status[0] = 0;
         return;
     }
     Unit u;
@@ -2577,14 +2580,14 @@ hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int c
 }
 
 hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, float *out, int rows, int cols,
-                         int units, hipStream_t s)
+                         int units, int *status, hipStream_t s)
 {
     const dim3 grid((units + 63) / 64, count);
     switch (fmt) {
-    case QMV_FMT_Q4_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q4_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
-    case QMV_FMT_Q6_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q6_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
-    case QMV_FMT_Q8_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q8_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
-    case QMV_FMT_Q5_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q5_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units); break;
+    case QMV_FMT_Q4_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q4_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units, status); break;
+    case QMV_FMT_Q6_K: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q6_K>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units, status); break;
+    case QMV_FMT_Q8_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q8_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units, status); break;
+    case QMV_FMT_Q5_0: hipLaunchKernelGGL(gather_rows_kernel<QMV_FMT_Q5_0>, grid, dim3(64), 0, s, w, ids, out, rows, cols, units, status); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

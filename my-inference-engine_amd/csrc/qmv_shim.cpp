@@ -1309,15 +1309,19 @@ QMV_API int qmv_device_matvec_argmax_f32(qmv_device_tensor tensor, const float *
 }
 
 QMV_API int qmv_device_embed_rows_f32(qmv_device_tensor t, const int *d_token_ids, int count, float *d_output,
-                                      void *stream)
+                                      int *d_status, void *stream)
 {
     if (t == nullptr || d_token_ids == nullptr || d_output == nullptr || count <= 0 || count > 65535) {
         set_error("invalid embedding gather arguments");
         return 0;
     }
     HIP_TRY(hipSetDevice(t->device));
+    hipStream_t s = (hipStream_t)stream;
+    /* The status starts at 1 (a fill kernel, so the call can be captured)
+     * and the gather clears it on an out-of-range id. */
+    if (d_status != nullptr) HIP_TRY(qmv::launch_fill_u32((unsigned *)d_status, 1, 1u, s));
     HIP_TRY(qmv::launch_gather(t->geo.format, t->data, d_token_ids, count, d_output, t->rows, t->cols, t->units,
-                               (hipStream_t)stream));
+                               d_status, s));
     return 1;
 }
 

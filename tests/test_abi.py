@@ -110,7 +110,7 @@ def test_invalid_sampler_and_device_args_fail_without_gpu(qmv):
     assert lib.qmv_device_matvec_f32(None, None, 1, None, None) == 0
     assert lib.qmv_device_greedy_argmax_f32(None, 10, None, None) == 0
     assert lib.qmv_device_matvec_argmax_f32(None, None, None, None, None) == 0
-    assert lib.qmv_device_embed_rows_f32(None, None, 1, None, None) == 0
+    assert lib.qmv_device_embed_rows_f32(None, None, 1, None, None, None) == 0
     assert lib.qmv_device_matvec_add_group_f32(None, 1, None, 1, None, None, None, None) == 0
     assert lib.qmv_device_matvec_swiglu_f32(None, None, None, 1, None, None) == 0
     assert lib.qmv_device_tensor_create(None, None) == 0

@@ -282,21 +282,23 @@ def test_random_shapes_match_oracle(qmv, oracle, gpu, t, rows, cols, batch, seed
 
 
 SWEEP_PLANS = [(0, 0, 0, 0)] * 6 + [(0, 2, 0, 0), (0, 0, 8, 0), (0, 0, 2, 0), (4096, 0, 0, 0), (0, 0, 0, 2),
-                                   (0, 1, 5, 0)]
+                                   (0, 1, 5, 0), (0, 0, 0, 20)]
 
 
 def test_random_sweep_with_plans(qmv, oracle, gpu):
     """600 seeded cases in one test: any format, 1..3000 rows, K up to 29
-    super-blocks or 119 blocks, batches of 1..40, under the default plan
-    (half the cases) or a forced one (units per wave, waves per group,
-    target waves, matrix cores from two positions)."""
+    super-blocks or 159 blocks of 32 (rows of up to 40 four-block units, so
+    the prefill plans for long rows run too), batches of 1..50, under the
+    default plan (half the cases) or a forced one (units per wave, waves per
+    group, target waves, matrix cores from two positions or only from 20, which
+    leaves tails of 9..19 positions to launches of 8)."""
     rng = np.random.default_rng(77)
     worst = 0.0
     for i in range(600):
         t = B.ALL_TYPES[int(rng.integers(0, 4))]
         rows = int(rng.choice([int(rng.integers(1, 200)), int(rng.integers(200, 3000))]))
-        cols = 256 * int(rng.integers(1, 30)) if t in (B.Q4_K, B.Q6_K) else 32 * int(rng.integers(1, 120))
-        batch = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32, 33, 40]))
+        cols = 256 * int(rng.integers(1, 30)) if t in (B.Q4_K, B.Q6_K) else 32 * int(rng.integers(1, 160))
+        batch = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16, 17, 24, 31, 32, 33, 40, 50]))
         plan = SWEEP_PLANS[int(rng.integers(0, len(SWEEP_PLANS)))]
         raw = qmv.synth_tensor(t, rows, cols, seed=20000 + i)
         x = qmv.synth_normal(batch * cols, seed=30000 + i).reshape(batch, cols)
@@ -640,15 +642,22 @@ def test_fused_argmax_ties_and_non_finite(qmv, gpu, hip):
 def test_embed_rows_bit_exact(qmv, oracle, gpu, hip, t, rows, cols):
     """Gathered rows (duplicates, first and last rows, rows of the partial last
     tile) equal the oracle's decode bit for bit; an out-of-range id gives a
-    NaN row and leaves the others exact."""
+    NaN row, leaves the others exact and clears the status word (which a call
+    with every id in range sets to 1, src/qwen2_architecture.cpp:384-393)."""
     raw = qmv.synth_tensor(t, rows, cols, seed=rows + 3)
     dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
     ids = np.array([0, rows - 1, 5, 5, rows // 2, rows - 2, 63 % rows, rows, -1, 1], dtype=np.int32)
     d_ids = hip.DeviceBuffer.from_array(ids)
     out = hip.DeviceBuffer(4 * ids.size * cols)
+    status = hip.DeviceBuffer(4)
     stream = hip.Stream()
-    qmv.device_embed_rows(dt, d_ids.ptr, ids.size, out.ptr, stream.handle)
+    status.fill(0x55)
+    qmv.device_embed_rows(dt, d_ids.ptr, 7, out.ptr, stream.handle, d_status=status.ptr)  # ids 0..6: in range
     stream.synchronize()
+    assert status.to_array(np.int32, (1,))[0] == 1
+    qmv.device_embed_rows(dt, d_ids.ptr, ids.size, out.ptr, stream.handle, d_status=status.ptr)
+    stream.synchronize()
+    assert status.to_array(np.int32, (1,))[0] == 0
     got = out.to_array(np.float32, (ids.size, cols))
     for i, r in enumerate(ids.tolist()):
         if 0 <= r < rows:

@@ -72,6 +72,22 @@ def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
     qmv.release_tensor(v.data)
 
 
+@pytest.mark.parametrize("t,rows,cols", [(B.Q8_0, 896, 4864), (B.Q5_0, 1536, 8960), (B.Q8_0, 200, 32 * 131),
+                                         (B.Q5_0, 130, 32 * 133)])
+@pytest.mark.parametrize("batch", [16, 27, 32])
+def test_prefill_long_rows_q5_q8(qmv, oracle, gpu, t, rows, cols, batch):
+    """Q8_0 / Q5_0 prefill launches over rows of 32 or more four-block units
+    (K >= 4096), where the plan takes three units per split for launches of
+    at most 8 tile groups and five otherwise; two shapes end in a partial
+    last unit (131 and 133 blocks)."""
+    raw = qmv.synth_tensor(t, rows, cols, seed=340 + batch)
+    x = qmv.synth_normal(batch * cols, seed=341 + batch).reshape(batch, cols)
+    v = qmv.make_view(raw, t, rows, cols)
+    y = qmv.matvec(v, x)
+    _check(oracle, raw, t, rows, cols, x, y, f"type {t} {rows}x{cols} B={batch}")
+    qmv.release_tensor(v.data)
+
+
 @pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K, B.Q5_0, B.Q8_0])
 @pytest.mark.parametrize("batch,parts", [(32, [16, 16]), (27, [9, 18]), (24, [12, 12]), (30, [10, 10, 10])])
 def test_prefill_positions_independent(qmv, gpu, hip, t, batch, parts):
