@@ -55,10 +55,12 @@ class QmvTensorView(ctypes.Structure):
 def make_view(buf: np.ndarray, ggml_type: int, rows: int, cols: int, offset: int = 0) -> QmvTensorView:
     """A consistent view of ``rows x cols`` packed weights at ``buf[offset:]``.
 
-    ``buf`` must stay alive while the view is used (the view borrows it, as the
-    reference's views borrow the GGUF mmap)."""
+    The view borrows ``buf``'s bytes, as the reference's views borrow the GGUF
+    mmap; it also holds a Python reference to ``buf`` so that a temporary array
+    passed straight in outlives the view."""
     be, bb = BLOCK_ELEMENTS[ggml_type], BLOCK_BYTES[ggml_type]
     v = QmvTensorView()
+    v._owner = buf
     v.data = buf.ctypes.data + offset
     v.ggml_type = ggml_type
     v.dimension_count = 2

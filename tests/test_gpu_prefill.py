@@ -175,7 +175,8 @@ def test_prefill_graph_replay(qmv, gpu, hip):
 
 
 def test_device_batch_limit(qmv, gpu, hip):
-    dt = qmv.DeviceTensor(qmv.make_view(qmv.synth_tensor(B.Q4_K, 64, 256, seed=350), B.Q4_K, 64, 256))
+    raw = qmv.synth_tensor(B.Q4_K, 64, 256, seed=350)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, 64, 256))
     dx = hip.DeviceBuffer(4 * 33 * 256)
     dy = hip.DeviceBuffer(4 * 33 * 64)
     with pytest.raises(qmv.QmvError):
