@@ -81,11 +81,45 @@ struct MatvecParams {
     int pair_waves;
 };
 
+/* One tensor of a row-major single-position launch (Q4_K): `w` holds the
+ * GGUF bytes of the tensor (row r at r * sb * 144), workgroups
+ * [wg_begin, next job's wg_begin) take `rows_per_wg` rows each. */
+struct RowdotJob {
+    const uint8_t *w;
+    float *y;
+    const float *add; /* optional: y[row] += add[row] */
+    int rows;
+    int wg_begin;
+};
+
+struct RowdotParams {
+    RowdotJob job[QMV_MAX_JOBS];
+    int njobs;
+    const float *x; /* K activations, shared by all jobs */
+    int sb;         /* super-blocks per row */
+    /* Fused greedy argmax (QMV_ROWDOT_ARGMAX): one candidate tile per
+     * workgroup, as MatvecParams describes. */
+    uint64_t *argmax_cand;
+    unsigned *argmax_count;
+    int *argmax_result;
+    int argmax_tiles;
+};
+
+/* Row-major epilogues. */
+#define QMV_ROWDOT_STORE 0
+#define QMV_ROWDOT_SWIGLU 1
+#define QMV_ROWDOT_ARGMAX 2
+
 /* Workspace of a fused argmax over `tiles` tiles (groups of 64 tiles). */
 inline size_t argmax_words(size_t tiles) { return tiles + (tiles + 63) / 64; }
 inline size_t argmax_counts(size_t tiles) { return (tiles + 63) / 64 + 1; }
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
+/* Row-major Q4_K launch at one position: `rows_per_wg` (2, 4 or 8) rows per
+ * workgroup of `waves` waves, `items` (1 or 2) 16-byte items per lane,
+ * epilogue `epi` (QMV_ROWDOT_*). */
+hipError_t launch_rowdot(const RowdotParams &p, int rows_per_wg, int items, int epi, int grid, int waves,
+                         hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
 /* status (may be null): cleared to 0 if any id is outside [0, rows). */

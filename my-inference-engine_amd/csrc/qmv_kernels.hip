@@ -825,7 +825,8 @@ __device__ __forceinline__ bool publish_and_count(uint64_t *slot, uint64_t c, un
 
 /* Workspace: argmax_cand[tiles + groups] (tile candidates, then group
  * candidates), argmax_count[groups + 1] (group counts, then the top count). */
-__device__ __forceinline__ void tile_argmax(const MatvecParams &p, int tile, bool valid, int row, float y, int lane)
+template <typename P>
+__device__ __forceinline__ void tile_argmax(const P &p, int tile, bool valid, int row, float y, int lane)
 {
     const int tiles = p.argmax_tiles;
     const int groups = (tiles + QMV_ARGMAX_GROUP - 1) / QMV_ARGMAX_GROUP;
@@ -2518,6 +2519,173 @@ rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, f
     }
 }
 
+/* ---- row-major single-position kernel (Q4_K) ---------------------------------
+ * For launches too small to fill the chip with 64-row tiles unless K is split
+ * across workgroups (whose publish / count / reload tail then dominates), a
+ * workgroup owns R whole rows instead, so no row is split across workgroups.
+ * It reads the GGUF row-major bytes directly: a Q4_K row is sb super-blocks of
+ * 144 bytes, a 16-byte header (d, dmin, 12 scale bytes) then 8 qs planes of 16
+ * bytes, all 16-byte aligned. Lane item i of a row is (super-block i / 8, plane
+ * i % 8): one 16-byte qs load plus the super-block's header (the same address
+ * for the 8 lanes of a super-block, one cache line). Item (s, p), g = p / 2,
+ * h = p % 2, holds weights 256s + 64g + 16h + [0, 16) in its low nibbles
+ * (sub-block 2g) and 256s + 64g + 32 + 16h + [0, 16) in its high nibbles
+ * (sub-block 2g + 1), so each lane keeps those 32 activations in registers
+ * and reuses them for its R rows; J items per lane cover rows of up to
+ * 8 * 64 * J / 8 super-blocks. A row's lane sums are added with DPP inside
+ * each wave, then across the workgroup's waves in wave order, so results are
+ * run-to-run identical. */
+
+/* Sum of v over the 64 lanes of a wave, identical in every lane: pairs, quads,
+ * 8s and 16s with DPP, then the four 16-lane rows in a fixed order. Every lane
+ * must be active. */
+template <int CTRL>
+__device__ __forceinline__ float dpp_plus(float v)
+{
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_total(float v)
+{
+    v = dpp_plus<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v = dpp_plus<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    v = dpp_plus<0x141>(v); /* row_half_mirror */
+    v = dpp_plus<0x140>(v); /* row_mirror */
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+/* EPI: QMV_ROWDOT_STORE (y = sum, plus `add` if set), QMV_ROWDOT_SWIGLU (jobs
+ * 0 = gate and 1 = up over the same rows in every workgroup; job 0's y gets
+ * up * silu(gate)), QMV_ROWDOT_ARGMAX (one job; y stored, then the greedy
+ * argmax of y with each workgroup as one candidate tile). */
+template <int R, int J, int EPI>
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowdot_q4k_kernel(RowdotParams p)
+{
+    constexpr int RS = EPI == QMV_ROWDOT_SWIGLU ? 2 * R : R; /* row slots: gate rows, then up rows */
+    __shared__ float red[QMV_MAX_WAVES][RS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
+    int j = 0;
+    if constexpr (EPI == QMV_ROWDOT_STORE)
+        while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const RowdotJob &job = p.job[j];
+    const int row0 = ((int)blockIdx.x - job.wg_begin) * R;
+    const int items = p.sb * 8;
+    const size_t row_bytes = (size_t)p.sb * 144;
+
+    float xv[J][32], xl[J], xh[J];
+    int qoff[J], hoff[J], gsel[J];
+    bool ok[J];
+    /* Lanes past the row's items repeat its last item (in-bounds loads, no
+     * branches) and drop their sums before the reduction. */
+#pragma unroll
+    for (int i = 0; i < J; ++i) {
+        const int it0 = tid + i * (int)blockDim.x;
+        ok[i] = it0 < items;
+        const int it = min(it0, items - 1);
+        const int s = it >> 3, pl = it & 7, g = pl >> 1, h = pl & 1;
+        gsel[i] = g;
+        qoff[i] = 144 * s + 16 + 16 * pl;
+        hoff[i] = 144 * s;
+        const int k0 = 256 * s + 64 * g + 16 * h;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 lo = *(const float4 *)(p.x + k0 + 4 * c);
+            const float4 hi = *(const float4 *)(p.x + k0 + 32 + 4 * c);
+            xv[i][4 * c] = lo.x; xv[i][4 * c + 1] = lo.y; xv[i][4 * c + 2] = lo.z; xv[i][4 * c + 3] = lo.w;
+            xv[i][16 + 4 * c] = hi.x; xv[i][17 + 4 * c] = hi.y; xv[i][18 + 4 * c] = hi.z; xv[i][19 + 4 * c] = hi.w;
+        }
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            a += xv[i][e];
+            b += xv[i][16 + e];
+        }
+        xl[i] = a;
+        xh[i] = b;
+    }
+
+    uint4 q[RS][J], hd[RS][J];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        const RowdotJob &jr = r < R ? job : p.job[1];
+        const uint8_t *base = jr.w + (size_t)min(row0 + r % R, jr.rows - 1) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < J; ++i) {
+            q[r][i] = ld16(base + qoff[i]);
+            hd[r][i] = ld16(base + hoff[i]);
+        }
+    }
+
+    float tot[RS];
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < J; ++i) {
+            /* low / high code sums scaled by 2^-24 (q4_dword_mix) */
+            float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                q4_dword_mix(word(q[r][i], e), xv[i] + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
+            const uint4 h = hd[r][i];
+            const bool upper = gsel[i] >= 2;
+            const uint32_t scw = upper ? (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u) : h.y & 0x3f3f3f3fu;
+            const uint32_t mw = upper ? ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u) : h.z & 0x3f3f3f3fu;
+            const int sh = (gsel[i] & 1) * 16;
+            const uint32_t scp = scw >> sh, mp = mw >> sh;
+            const float d24 = f16_bits_to_f32(h.x) * 16777216.0f, dmin = f16_bits_to_f32(h.x >> 16);
+            /* d * sc is exact (11 x 6 significant bits); the power-of-2
+             * factors (2^24, 1/16 for high codes used as 16q) are exact. */
+            float c = (d24 * ubyte(scp, 0)) * (l0 + l1);
+            c = fmaf(d24 * ubyte(scp, 1) * 0.0625f, h0 + h1, c);
+            c = fmaf(-(dmin * ubyte(mp, 0)), xl[i], c);
+            c = fmaf(-(dmin * ubyte(mp, 1)), xh[i], c);
+            if (ok[i]) acc = i == 0 ? c : acc + c;
+        }
+        tot[r] = wave_total(acc);
+    }
+
+    if (nw > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < RS; ++r) red[wave][r] = tot[r];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int r = 0; r < RS; ++r) {
+            float s = red[0][r];
+            for (int v = 1; v < nw; ++v) s += red[v][r];
+            tot[r] = s;
+        }
+    }
+    /* Lane r < R emits row row0 + r. */
+    float out = tot[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+        if (lane == r) out = tot[r];
+    const int row = row0 + lane;
+    const bool valid = lane < R && row < job.rows;
+    if constexpr (EPI == QMV_ROWDOT_SWIGLU) {
+        float up = tot[R];
+#pragma unroll
+        for (int r = 1; r < R; ++r)
+            if (lane == r) up = tot[R + r];
+        if (valid) {
+            if (job.add != nullptr) out += job.add[row];
+            if (p.job[1].add != nullptr) up += p.job[1].add[row];
+            job.y[row] = swiglu_value(out, up);
+        }
+    } else {
+        if (valid) {
+            if (job.add != nullptr) out += job.add[row];
+            job.y[row] = out;
+        }
+        if constexpr (EPI == QMV_ROWDOT_ARGMAX) tile_argmax(p, (int)blockIdx.x, valid, row, out, lane);
+    }
+}
+
 /* ---- host-side launchers -------------------------------------------------- */
 
 template <int FMT, int M>
@@ -2560,6 +2728,24 @@ hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int wa
     case QMV_FMT_Q5_0: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q5_0) break;
     default: break;
     }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_rowdot(const RowdotParams &p, int rows_per_wg, int items, int epi, int grid, int waves,
+                         hipStream_t s)
+{
+    if (waves < 1 || waves > QMV_MAX_WAVES || grid < 1) return hipErrorInvalidValue;
+#define QMV_ROWDOT(R, J, E)                                                                            \
+    if (rows_per_wg == R && items == J && epi == E) {                                                  \
+        hipLaunchKernelGGL((rowdot_q4k_kernel<R, J, E>), dim3(grid), dim3(waves * 64), 0, s, p);       \
+        return hipGetLastError();                                                                      \
+    }
+#define QMV_ROWDOT_E(R, J) QMV_ROWDOT(R, J, QMV_ROWDOT_STORE) QMV_ROWDOT(R, J, QMV_ROWDOT_SWIGLU)           \
+    QMV_ROWDOT(R, J, QMV_ROWDOT_ARGMAX)
+    QMV_ROWDOT_E(2, 1) QMV_ROWDOT_E(4, 1) QMV_ROWDOT_E(8, 1) QMV_ROWDOT_E(2, 2) QMV_ROWDOT_E(4, 2)
+    QMV_ROWDOT_E(8, 2)
+#undef QMV_ROWDOT_E
+#undef QMV_ROWDOT
     return hipErrorInvalidValue;
 }
 

@@ -46,6 +46,7 @@ struct QmvDeviceTensor {
     int units, tiles;
     uint64_t packed_bytes, device_bytes;
     uint8_t *data;
+    uint8_t *rowmajor; /* Q4_K: the GGUF bytes as well (row-major kernel), else null */
 };
 
 namespace {
@@ -339,20 +340,56 @@ int grow_device(float **p, size_t *cap, size_t n)
     return 1;
 }
 
+int env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+/* Row-major single-position kernel for small Q4_K launches
+ * (rowdot_q4k_kernel): QMV_ROWDOT = 0 turns it off (read at start-up, before
+ * tensors are uploaded); QMV_ROWDOT_ROWS = rows per workgroup (2, 4 or 8).
+ * Measured on MI355X in a graph of the Qwen2.5-7B decode set, us per launch
+ * (tiled / rows per workgroup 2, 4, 8): q|k|v 6.81 / 6.11, 6.74, 7.73; o
+ * 5.80 / 5.10, 5.49, 7.02; gate|up 18.5 / 26.4, 23.6, 23.1. Every workgroup
+ * reads the row's whole activation vector, so the kernel pays only where the
+ * tiled plan would split K across workgroups to fill the chip at all. */
+std::atomic<int> g_rowdot{env_int("QMV_ROWDOT", 1)};
+std::atomic<int> g_rowdot_rows{env_int("QMV_ROWDOT_ROWS", 2)};
+
+/* Super-blocks per row the row-major kernel takes: 8 waves x 64 lanes x 2
+ * items, 8 items per super-block. */
+constexpr int kRowdotMaxSb = QMV_MAX_WAVES * 64 * 2 / 8;
+/* Launches of at most this many tiled (64-row tile, K-unit) pairs, summed over
+ * the launch's tensors, run row-major: Qwen2.5-7B q|k|v (1008) and o (784),
+ * not gate|up (8288). */
+constexpr long long kRowdotMaxUnits = 2048;
+
+long long tiled_units(int rows, int blocks_per_row)
+{
+    return (long long)((rows + QMV_TILE_ROWS - 1) / QMV_TILE_ROWS) * blocks_per_row;
+}
+
+/* Whether an upload also keeps the GGUF bytes for the row-major kernel. */
+bool keeps_rowmajor(const QmvGeometry &geo, int rows, int blocks_per_row)
+{
+    return g_rowdot.load() != 0 && geo.format == QMV_FMT_Q4_K && blocks_per_row <= kRowdotMaxSb &&
+           tiled_units(rows, blocks_per_row) <= kRowdotMaxUnits;
+}
+
 /* ---- upload ------------------------------------------------------------------- */
 
 void tensor_free(QmvDeviceTensor *t)
 {
     if (!t) return;
-    if (t->data) {
+    if (t->data || t->rowmajor) {
         int cur = 0;
-        if (hipGetDevice(&cur) == hipSuccess && cur != t->device) {
-            if (hipSetDevice(t->device) == hipSuccess) {
-                (void)hipFree(t->data);
-                (void)hipSetDevice(cur);
-            }
-        } else {
-            (void)hipFree(t->data);
+        const bool other = hipGetDevice(&cur) == hipSuccess && cur != t->device;
+        if (!other || hipSetDevice(t->device) == hipSuccess) {
+            if (t->data) (void)hipFree(t->data);
+            if (t->rowmajor) (void)hipFree(t->rowmajor);
+            if (other) (void)hipSetDevice(cur);
         }
     }
     delete t;
@@ -372,6 +409,7 @@ int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_
     t->packed_bytes = (uint64_t)s.rows * (uint64_t)s.blocks_per_row * (uint64_t)s.geo.block_bytes;
     t->device_bytes = (uint64_t)t->tiles * (uint64_t)t->units * QMV_TILE_ROWS * (uint64_t)s.geo.unit_bytes;
     t->data = nullptr;
+    t->rowmajor = nullptr;
 
     uint8_t *raw = nullptr;
     HIP_TRY(counted_malloc((void **)&raw, t->packed_bytes));
@@ -382,6 +420,10 @@ int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_
     HIP_TRY(qmv::launch_repack(s.geo.format, raw, t->data, s.rows, s.blocks_per_row, t->units,
                                s.geo.blocks_per_unit, s.geo.block_bytes, s.geo.unit_bytes, t->tiles, stream));
     HIP_TRY(hipStreamSynchronize(stream));
+    if (keeps_rowmajor(s.geo, s.rows, s.blocks_per_row)) {
+        t->rowmajor = raw_guard.release();
+        t->device_bytes += t->packed_bytes;
+    }
     *out = t.release();
     return 1;
 }
@@ -443,13 +485,6 @@ std::shared_ptr<QmvDeviceTensor> cached_tensor(const QmvTensorView *m, const Sha
 }
 
 /* ---- launch planning ------------------------------------------------------------- */
-
-int env_int(const char *name, int dflt)
-{
-    const char *v = getenv(name);
-    if (!v || !*v) return dflt;
-    return atoi(v);
-}
 
 std::atomic<int> g_target_waves{env_int("QMV_TARGET_WAVES", 0)};
 std::atomic<int> g_force_u{env_int("QMV_UNITS_PER_WAVE", 0)};
@@ -624,6 +659,9 @@ Plan plan_prefill(long long groups, int units)
  * entry point). */
 struct ChunkPlan {
     qmv::MatvecParams p;
+    qmv::RowdotParams rp;                  /* row-major launch (rowdot): its parameters */
+    bool rowdot = false;
+    int rd_rows = 0, rd_items = 0, rd_epi = 0; /* rows per workgroup, 16-byte items per lane, epilogue */
     bool prefill = false, paired = false;
     int mt = 1, grid = 0, waves = 0, fmt = 0;
     size_t partials = 0, counters = 0;     /* floats / words of split-K workspace */
@@ -631,10 +669,70 @@ struct ChunkPlan {
     size_t argmax_tiles = 0;               /* fused argmax candidate slots needed (0: none) */
 };
 
+/* A single-position launch of Q4_K tensors on the row-major kernel: every
+ * tensor keeps its GGUF bytes, rows fit 8 waves of 2 items per lane, and the
+ * epilogue is at most an added vector. */
+bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
+                 const Epilogue &epi, ChunkPlan *cp)
+{
+    if (g_rowdot.load() == 0 || count > QMV_MAX_JOBS) return false;
+    const QmvDeviceTensor *t0 = ts[0];
+    long long units = 0;
+    for (int i = 0; i < count; ++i) {
+        if (ts[i]->rowmajor == nullptr || ts[i]->cols != t0->cols) return false;
+        units += tiled_units(ts[i]->rows, ts[i]->blocks_per_row);
+    }
+    if (units > kRowdotMaxUnits) return false;
+    if (epi.swiglu && (count != 2 || ts[1]->rows != t0->rows)) return false; /* rejected by the tiled plan */
+    if (epi.argmax && (count != 1 || b0 != 0)) return false;
+    const int sb = t0->blocks_per_row, items = 8 * sb;
+    if (sb > kRowdotMaxSb) return false;
+    const int per_lane = items <= QMV_MAX_WAVES * 64 ? 1 : 2;
+    const int waves = (items + 64 * per_lane - 1) / (64 * per_lane);
+    const int want = g_rowdot_rows.load();
+    const int R = want == 2 || want == 8 ? want : 4;
+    qmv::RowdotParams &rp = cp->rp;
+    memset(&rp, 0, sizeof rp);
+    rp.njobs = count;
+    rp.x = d_in + (size_t)b0 * t0->cols;
+    rp.sb = sb;
+    long long wg = 0;
+    for (int i = 0; i < count; ++i) {
+        qmv::RowdotJob &j = rp.job[i];
+        j.w = ts[i]->rowmajor;
+        j.y = d_out[i] + (size_t)b0 * ts[i]->rows;
+        j.rows = ts[i]->rows;
+        j.wg_begin = (int)wg;
+        if (epi.add && epi.add[i]) j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
+        if (!epi.swiglu || i == 0) wg += (ts[i]->rows + R - 1) / R; /* SwiGLU: both jobs in each workgroup */
+    }
+    if (wg > INT_MAX) return false;
+    memset(&cp->p, 0, sizeof cp->p);
+    cp->rowdot = true;
+    cp->rd_rows = R;
+    cp->rd_items = per_lane;
+    cp->rd_epi = epi.swiglu ? QMV_ROWDOT_SWIGLU : epi.argmax ? QMV_ROWDOT_ARGMAX : QMV_ROWDOT_STORE;
+    if (epi.argmax) {
+        rp.argmax_result = epi.argmax;
+        rp.argmax_tiles = (int)wg;
+    }
+    cp->prefill = cp->paired = false;
+    cp->mt = 1;
+    cp->grid = (int)wg;
+    cp->waves = waves;
+    cp->fmt = t0->geo.format;
+    cp->partials = cp->counters = 0;
+    cp->pair_vals = cp->pair_count = 0;
+    cp->argmax_tiles = epi.argmax ? (size_t)wg : 0;
+    return true;
+}
+
 int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, int batch, float *const *d_out,
                const Epilogue &epi, ChunkPlan *cp)
 {
     const QmvDeviceTensor *t0 = ts[0];
+    cp->rowdot = false;
+    if (batch == 1 && plan_rowdot(ts, count, d_in, b0, d_out, epi, cp)) return 1;
     const bool mfma = use_matrix_cores(t0->geo.format, batch);
     /* Up to 8 positions: the matvec kernels for exactly `batch` positions.
      * More: the prefill kernel, 16 or 32 position rows with the batch in the
@@ -774,7 +872,9 @@ void bind_workspace(ChunkPlan &cp, float *partials, unsigned *counters)
 
 int enqueue_chunk(const ChunkPlan &cp, hipStream_t stream)
 {
-    if (cp.prefill)
+    if (cp.rowdot)
+        HIP_TRY(qmv::launch_rowdot(cp.rp, cp.rd_rows, cp.rd_items, cp.rd_epi, cp.grid, cp.waves, stream));
+    else if (cp.prefill)
         HIP_TRY(qmv::launch_prefill(cp.fmt, cp.p, cp.mt, cp.grid, stream));
     else
         HIP_TRY(qmv::launch_matvec(cp.fmt, cp.p, cp.mt, cp.grid, cp.waves, stream));
@@ -793,8 +893,8 @@ int launch_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     bind_workspace(cp, ws.partials, ws.counters);
     if (cp.argmax_tiles) {
         if (!workspace_fused_argmax(ws, stream, cp.argmax_tiles)) return 0;
-        cp.p.argmax_cand = ws.fused_cand;
-        cp.p.argmax_count = ws.fused_count;
+        cp.p.argmax_cand = cp.rp.argmax_cand = ws.fused_cand;
+        cp.p.argmax_count = cp.rp.argmax_count = ws.fused_count;
     }
     return enqueue_chunk(cp, stream);
 }

@@ -1,0 +1,195 @@
+"""GPU parity of the row-major single-position kernel (small Q4_K launches),
+through the C ABI.
+
+Q4_K tensors whose tiled plan covers at most 2048 (64-row tile, 256-weight
+unit) pairs keep their GGUF bytes on the device as well, and their
+single-position launches run row-major: a workgroup owns whole rows, lanes
+split K, and a row's sums are added inside the workgroup. The bars are those
+of the tiled path:
+  * rows: |y - y_oracle| <= 1e-5 * sum_k |w_k x_k| (the reference's scalar
+    row loop, src/quantized_matvec.cpp:152-158, restated by the oracle);
+  * the addend: bit-identical to the plain launch's rows plus the addend;
+  * SwiGLU: bit-identical to up * silu(gate) of the plain launch's rows
+    computed by the same device expression, and within 4 ulp of the
+    oracle's transformer_swiglu_f32;
+  * fused argmax: logits bit-identical to the plain launch, index equal to
+    the greedy argmax of those logits;
+  * repeated launches are bit-identical.
+"""
+import numpy as np
+import pytest
+
+import _blocks as B
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+SWIGLU_ULPS = 4
+SMALL_UNITS = 2048  # tiled (tile, unit) pairs up to which a launch runs row-major
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def hip(qmv):
+    import importlib
+    return importlib.import_module("my-inference-engine_amd.hip_runtime")
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def _tiled_units(rows, cols):
+    return -(-rows // 64) * (cols // 256)
+
+
+def _device(qmv, rows, cols, seed):
+    raw = qmv.synth_tensor(B.Q4_K, rows, cols, seed=seed)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, rows, cols))
+    tiled = -(-rows // 64) * (cols // 256) * 64 * 144
+    packed = rows * (cols // 256) * 144
+    small = _tiled_units(rows, cols) <= SMALL_UNITS and cols // 256 <= 128
+    # the extra GGUF copy is what routes the tensor's single-position launches
+    assert dt.device_bytes == tiled + (packed if small else 0), (rows, cols, dt.device_bytes)
+    return raw, dt
+
+
+def _check(oracle, raw, rows, cols, x, y, what):
+    y_ref = oracle.matvec(raw, B.Q4_K, rows, cols, x)
+    _, absdot = oracle.row_stats(raw, B.Q4_K, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - y_ref)
+    bad = err > TOL * absdot
+    assert not bad.any(), f"{what}: {int(bad.sum())} rows over tolerance"
+    return float(np.max(err / np.maximum(absdot, 1e-300)))
+
+
+# rows: odd counts (a workgroup's second row missing), one row, tile edges;
+# K: 1 super-block, a fraction of a wave (6), more than a wave (14, 35), eight
+# full waves (64), and two items per lane (65, 100, 128).
+SHAPES = [(1, 256), (2, 256), (3, 512), (63, 1536), (64, 1536), (65, 3584), (513, 3584), (3584, 3584),
+          (257, 35 * 256), (130, 64 * 256), (64, 65 * 256), (131, 100 * 256), (1, 128 * 256), (128, 128 * 256)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_rowmajor_matches_oracle(qmv, oracle, gpu, hip, rows, cols):
+    log(f"row-major Q4_K {rows}x{cols}")
+    raw, dt = _device(qmv, rows, cols, seed=700 + rows + cols // 256)
+    assert _tiled_units(rows, cols) <= SMALL_UNITS
+    x = qmv.synth_normal(cols, seed=701 + rows)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(4 * rows)
+    with hip.Stream() as s:
+        dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+        s.synchronize()
+        y = dy.to_array(np.float32, (rows,))
+        worst = _check(oracle, raw, rows, cols, x, y, f"{rows}x{cols}")
+        for _ in range(2):
+            dy.fill(0)
+            dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+            s.synchronize()
+            assert np.array_equal(_bits(dy.to_array(np.float32, (rows,))), _bits(y))
+    log(f"  worst err/sum|wx| = {worst:.2e}")
+    dt.close()
+
+
+def test_rowmajor_group_of_unequal_rows(qmv, oracle, gpu, hip):
+    """q|k|v-shaped group (Qwen2.5-7B): three tensors of 3584, 512 and 512 rows
+    over one input, one launch."""
+    cols = 3584
+    specs = [(3584, 710), (512, 711), (512, 712)]
+    tensors = [_device(qmv, r, cols, seed) for r, seed in specs]
+    x = qmv.synth_normal(cols, seed=713)
+    dx = hip.DeviceBuffer.from_array(x)
+    outs = [hip.DeviceBuffer(4 * r) for r, _ in specs]
+    with hip.Stream() as s:
+        qmv.device_matvec_group([dt for _, dt in tensors], dx.ptr, 1, [o.ptr for o in outs], s.handle)
+        s.synchronize()
+        for (raw, dt), (r, _), o in zip(tensors, specs, outs):
+            _check(oracle, raw, r, cols, x, o.to_array(np.float32, (r,)), f"group {r}x{cols}")
+            alone = hip.DeviceBuffer(4 * r)
+            dt.matvec(dx.ptr, 1, alone.ptr, s.handle)
+            s.synchronize()
+            assert np.array_equal(_bits(alone.to_array(np.float32, (r,))), _bits(o.to_array(np.float32, (r,))))
+    for _, dt in tensors:
+        dt.close()
+
+
+def test_rowmajor_addend_bit_exact(qmv, oracle, gpu, hip):
+    cols = 1536
+    specs = [(1536, 720), (256, 721), (255, 722)]
+    tensors = [_device(qmv, r, cols, seed) for r, seed in specs]
+    x = qmv.synth_normal(cols, seed=723)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        plain = [hip.DeviceBuffer(4 * r) for r, _ in specs]
+        qmv.device_matvec_group([dt for _, dt in tensors], dx.ptr, 1, [p.ptr for p in plain], s.handle)
+        adds = [qmv.synth_normal(r, seed=724 + i) for i, (r, _) in enumerate(specs)]
+        dadds = [hip.DeviceBuffer.from_array(a) for a in adds]
+        outs = [hip.DeviceBuffer(4 * r) for r, _ in specs]
+        qmv.device_matvec_add_group([dt for _, dt in tensors], dx.ptr, 1, [d.ptr for d in dadds],
+                                    [0] * len(specs), [o.ptr for o in outs], s.handle)
+        s.synchronize()
+        for (r, _), p, a, o in zip(specs, plain, adds, outs):
+            want = p.to_array(np.float32, (r,)) + a
+            assert np.array_equal(_bits(o.to_array(np.float32, (r,))), _bits(want))
+    for _, dt in tensors:
+        dt.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (65, 512), (896, 3584), (1000, 1536)])
+def test_rowmajor_swiglu(qmv, oracle, gpu, hip, rows, cols):
+    log(f"row-major SwiGLU {rows}x{cols}")
+    raw_g, dg = _device(qmv, rows, cols, 730)
+    raw_u, du = _device(qmv, rows, cols, 731)
+    x = qmv.synth_normal(cols, seed=732)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        g = hip.DeviceBuffer(4 * rows)
+        u = hip.DeviceBuffer(4 * rows)
+        qmv.device_matvec_group([dg, du], dx.ptr, 1, [g.ptr, u.ptr], s.handle)
+        out = hip.DeviceBuffer(4 * rows)
+        qmv.device_matvec_swiglu(dg, du, dx.ptr, 1, out.ptr, s.handle)
+        s.synchronize()
+        gate, up = g.to_array(np.float32, (rows,)), u.to_array(np.float32, (rows,))
+        _check(oracle, raw_g, rows, cols, x, gate, "gate")
+        _check(oracle, raw_u, rows, cols, x, up, "up")
+        got = out.to_array(np.float32, (rows,)).astype(np.float64)
+        ok, ref = oracle.swiglu(gate, up)
+        assert ok == 1
+        ref = np.asarray(ref, dtype=np.float64)
+        assert (np.abs(got - ref) <= SWIGLU_ULPS * 2.0 ** -23 * np.abs(ref) + 1e-30).all()
+    dg.close()
+    du.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (7, 512), (1000, 3584), (4099, 1536)])
+def test_rowmajor_fused_argmax(qmv, oracle, gpu, hip, rows, cols):
+    log(f"row-major fused argmax {rows}x{cols}")
+    raw, dt = _device(qmv, rows, cols, 740 + rows)
+    x = qmv.synth_normal(cols, seed=741)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        plain = hip.DeviceBuffer(4 * rows)
+        dt.matvec(dx.ptr, 1, plain.ptr, s.handle)
+        logits = hip.DeviceBuffer(4 * rows)
+        res = hip.DeviceBuffer(8)
+        for _ in range(3):  # the candidate counters must be left at zero
+            qmv.device_matvec_argmax(dt, dx.ptr, logits.ptr, res.ptr, s.handle)
+            s.synchronize()
+            y = logits.to_array(np.float32, (rows,))
+            assert np.array_equal(_bits(y), _bits(plain.to_array(np.float32, (rows,))))
+            token, finite = res.to_array(np.int32, (2,))
+            assert finite == 1 and token == int(np.argmax(y)), (token, int(np.argmax(y)))
+        _check(oracle, raw, rows, cols, x, y, "logits")
+    dt.close()
+
+
+def test_large_launch_keeps_tiled_layout_only(qmv, gpu):
+    """Gate-sized tensors (Qwen2.5-7B, 18944 x 3584) stay tiled: no extra copy."""
+    raw = qmv.synth_tensor(B.Q4_K, 18944, 3584, seed=750)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, 18944, 3584))
+    assert dt.device_bytes == 296 * 14 * 64 * 144
+    dt.close()
