@@ -717,21 +717,29 @@ __device__ __forceinline__ void store_partial(float *p, float v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* Sum of the n partials part[i * stride] (i = 0..n-1, this lane's element),
- * added in index order. Loads go out in batches of 16 before any is waited
- * for, so a sum costs ceil(n / 16) memory round trips. */
-__device__ __forceinline__ float sum_partials(const float *part, size_t stride, int n)
+/* Sums of the n partials of M elements: sum[m] = part[m * 64] + part[stride +
+ * m * 64] + ... + part[(n - 1) * stride + m * 64] (this lane's elements),
+ * each added in split order. The loads of a batch of splits for all M
+ * elements go out before any is waited for (about LOADS in flight: 16 keeps
+ * the VALU kernels' registers, 64 fits the matrix-core kernel's), so the sums
+ * cost ceil(n / batch) memory round trips rather than M times that. */
+template <int M, int LOADS>
+__device__ __forceinline__ void sum_partials(const float *part, size_t stride, int n, float (&sum)[M])
 {
-    float s = 0.0f;
-    for (int b = 0; b < n; b += 16) {
-        float v[16];
+    constexpr int B = LOADS / M > 1 ? LOADS / M : 1;
+    for (int b = 0; b < n; b += B) {
+        float v[B][M];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = b + i < n ? load_partial(part + (size_t)(b + i) * stride) : 0.0f;
+        for (int i = 0; i < B; ++i)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (b + i < n) s = b + i == 0 ? v[i] : s + v[i];
+            for (int m = 0; m < M; ++m)
+                v[i][m] = b + i < n ? load_partial(part + (size_t)(b + i) * stride + m * 64) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < B; ++i)
+            if (b + i < n)
+#pragma unroll
+                for (int m = 0; m < M; ++m) sum[m] = b + i == 0 ? v[i][m] : sum[m] + v[i][m];
     }
-    return s;
 }
 
 /* ---- matvec kernel ---------------------------------------------------------
@@ -991,8 +999,10 @@ __device__ __forceinline__ void finish_paired(const MatvecParams &p, const WgWor
         prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
         if (prev != (unsigned)S - 1u) return;
         asm volatile("" ::: "memory");
-        g = sum_partials(part, 128, S);
-        u = sum_partials(part + 64, 128, S);
+        float gu[2];
+        sum_partials<2, 16>(part, 128, S, gu);
+        g = gu[0];
+        u = gu[1];
         if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const int row = w.tile * 64 + lane;
@@ -1003,7 +1013,7 @@ __device__ __forceinline__ void finish_paired(const MatvecParams &p, const WgWor
     }
 }
 
-template <int M>
+template <int M, int LOADS = 16>
 __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork &w, int nwaves, int lane,
                                             const float (*red)[M][64], int npos = M)
 {
@@ -1033,8 +1043,7 @@ __device__ __forceinline__ void finish_tile(const MatvecParams &p, const WgWork 
         prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
         if (prev != (unsigned)job.splits - 1u) return;
         asm volatile("" ::: "memory");
-#pragma unroll
-        for (int m = 0; m < M; ++m) sum[m] = sum_partials(part + m * 64 + lane, (size_t)M * 64, job.splits);
+        sum_partials<M, LOADS>(part + lane, (size_t)M * 64, job.splits, sum);
         if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     /* One copy of the row epilogue serves both paths. */
@@ -1258,22 +1267,25 @@ __device__ __forceinline__ void q4k_unit_mfma(const uint8_t *slab, const float *
     for (int g = 0; g < 4; ++g) q[(SB0 >> 1) & 1][g] = *(const uint2 *)(qsp + (SB0 >> 1) * 2048 + g * 256);
     const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
                            (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
-    float xv[2][8];
-    load_x<8>(xv[SB0 & 1], (gf32 *)(xp + 32 * SB0));
+    /* Activations run two sub-blocks ahead (a ring of three): one sub-block of
+     * compute does not cover an L2 round trip. */
+    float xv[3][8];
+    load_x<8>(xv[SB0 % 3], (gf32 *)(xp + 32 * SB0));
+    if (SB0 + 1 < SB1) load_x<8>(xv[(SB0 + 1) % 3], (gf32 *)(xp + 32 * (SB0 + 1)));
 #pragma unroll
     for (int sb = SB0; sb < SB1; ++sb) {
         const int c = sb >> 1;
         const bool high = sb & 1;
-        /* Next sub-block's activations, and at a group's start the next
-         * group's codes, load while this sub-block runs. */
-        if (sb + 1 < SB1) load_x<8>(xv[(sb + 1) & 1], ptr_after(xp + 32 * (sb + 1), acc[0][0]));
+        /* The activations of sub-block sb + 2, and at a group's start the
+         * next group's codes, load while this sub-block runs. */
+        if (sb + 2 < SB1) load_x<8>(xv[(sb + 2) % 3], ptr_after(xp + 32 * (sb + 2), acc[0][0]));
         if (!high && c + 1 < SB1 / 2) {
             gu8 *nq = bytes_after(qsp + (c + 1) * 2048, acc[1][0]);
 #pragma unroll
             for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
         }
         bf16x8_t a0, a1, a2;
-        x_limbs<8>(xv[sb & 1], true, a0, a1, a2);
+        x_limbs<8>(xv[sb % 3], true, a0, a1, a2);
         bf16x8_t b[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
@@ -1506,17 +1518,17 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
         w[PR0 & 1][g][1] = *(const uint32_t *)(wp + (4 * G0 + 2 + H0) * 1024 + g * 256);
         w[PR0 & 1][g][2] = *(const uint32_t *)(wp + (8 + 2 * G0 + H0) * 1024 + g * 256);
     }
-    float xv[2][4];
-    load_x<4>(xv[T0 & 1], (gf32 *)(xp + 16 * (8 * G0 + H0)));
+    /* Activations of step t (sub-block j(t)) run two steps ahead. */
+    auto sub_of = [](int t) { return 8 * (t >> 3) + 2 * (t & 3) + ((t >> 2) & 1); };
+    float xv[3][4];
+    load_x<4>(xv[T0 % 3], (gf32 *)(xp + 16 * sub_of(T0)));
+    if (T0 + 1 < T1) load_x<4>(xv[(T0 + 1) % 3], (gf32 *)(xp + 16 * sub_of(T0 + 1)));
 #pragma unroll
     for (int t = T0; t < T1; ++t) {
         const int pr = t >> 2, r = t & 3; /* pair (G, hf) = (pr >> 1, pr & 1) */
         const int G = pr >> 1, hf = pr & 1;
         const int j = 8 * G + 2 * r + hf;
-        if (t + 1 < T1) {
-            const int tn = t + 1, jn = 8 * (tn >> 3) + 2 * (tn & 3) + ((tn >> 2) & 1);
-            load_x<4>(xv[(t + 1) & 1], ptr_after(xp + 16 * jn, acc[0][0]));
-        }
+        if (t + 2 < T1) load_x<4>(xv[(t + 2) % 3], ptr_after(xp + 16 * sub_of(t + 2), acc[0][0]));
         if (r == 0 && pr + 1 < PR0 + NPR) {
             const int Gn = (pr + 1) >> 1, hn = (pr + 1) & 1;
             gu8 *np = bytes_after(wp, acc[1][0]);
@@ -1528,7 +1540,7 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
             }
         }
         bf16x4_t a0, a1, a2;
-        x_limbs<4>(xv[t & 1], true, a0, a1, a2);
+        x_limbs<4>(xv[t % 3], true, a0, a1, a2);
         bf16x4_t bl[4], bh[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
@@ -1630,7 +1642,7 @@ matvec_mfma_kernel(MatvecParams p)
             if (4 * kc + j < M) red[wave][4 * kc + j][16 * g + n] = acc[g][j];
     __syncthreads();
     if (wave != 0) return;
-    finish_tile<M>(p, w, blockDim.x >> 6, lane, red);
+    finish_tile<M, 64>(p, w, blockDim.x >> 6, lane, red);
 }
 
 /* ---- Prefill batches (9..32 positions), all four formats: GEMM-shaped -------
