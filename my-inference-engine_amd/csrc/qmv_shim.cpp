@@ -585,17 +585,18 @@ Plan plan_for(long long total_tiles, int units, int long_waves, int short_waves,
     return p;
 }
 
-/* Work items per K-unit on the matrix-core kernel (M <= 8). Measured at
- * M = 8 on the Qwen2.5-7B layer shapes (us per launch, parts 1 / 2 / 4):
- * q|k|v 16.2 / 13.4 / 15.0, o 13.4 / 12.8 / 14.1, gate|up 46.3 / 44.5 / 62.3,
- * down (74 units per row) 45.1 / 51.7 / 64.6. Halves pay on rows of few
- * units, where a unit per wave leaves about one wave per SIMD; more items
- * cost more split-K partials than they gain, so quarters are not built. */
-int mfma_parts(int units)
+/* Work items per K-unit on the matrix-core kernel (M <= 8): halves pay on
+ * small launches over rows of few units, where a unit per wave leaves about
+ * one wave per SIMD. Measured at M = 8 on the Qwen2.5-7B layer shapes (us per
+ * launch, whole / half / quarter units): q|k|v (72 tiles x 14 units) 11.9 /
+ * 10.8 / 12.4, o (56 x 14) 9.4 / 9.9 / 11.4, gate|up (592 x 14) 34.0 / 36.3 /
+ * 50.8, down (56 x 74) 33.8 / 36.1 / 48.3. More items cost more split-K
+ * partials than they gain, so quarters are not built. */
+int mfma_parts(int units, long long total_tiles)
 {
     const int forced = g_mfma_parts.load();
     if (forced == 1 || forced == 2) return forced;
-    return units < 32 ? 2 : 1;
+    return units < 32 && total_tiles * units <= 1024 ? 2 : 1;
 }
 
 /* Work items per K-unit on the VALU kernels for batches (M >= 2): halves.
@@ -748,7 +749,7 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
         total_tiles += ts[i]->tiles;
         total_groups += (ts[i]->tiles + QMV_PF_TILES - 1) / QMV_PF_TILES;
     }
-    const int parts = prefill ? 1 : mfma ? mfma_parts(t0->units) : batch >= 2 ? valu_parts(t0->units) : 1;
+    const int parts = prefill ? 1 : mfma ? mfma_parts(t0->units, total_tiles) : batch >= 2 ? valu_parts(t0->units) : 1;
     /* Single-position launches of many units (the vocabulary projection:
      * 33236) run several rounds of resident waves; five waves per workgroup
      * (three splits of 14 units instead of four) measured 80.9 us against

@@ -88,24 +88,25 @@ def test_formats_and_batches(qmv, gpu, hip, t, rows, cols, batch):
 
 
 def test_vocab_shape_and_oversized_call(qmv, gpu, hip):
-    """151936 x 3584 Q6_K fits for one position; at 8 positions its split-K
-    partials exceed the scratch, so the call fails and writes nothing."""
-    rows, cols = 151936, 3584
+    """151936 x 3584 Q6_K fits for one position; at 32 positions its split-K
+    partials (2374 tiles x 3 splits x 32 position rows x 64 floats, 58 MB)
+    exceed the scratch, so the call fails and writes nothing."""
+    rows, cols, big = 151936, 3584, 32
     with hip.Stream() as stream:
         dts = _tensors(qmv, B.Q6_K, [rows], cols, seed=540)
         log("noalloc: Q6_K 151936x3584, M=1")
         _run_both(qmv, hip, dts, 1, seed=541, stream=stream)
-        x = qmv.synth_normal(8 * cols, seed=542)
+        x = qmv.synth_normal(big * cols, seed=542)
         dx = hip.DeviceBuffer.from_array(x)
-        dy = hip.DeviceBuffer(4 * 8 * rows)
+        dy = hip.DeviceBuffer(4 * big * rows)
         dy.fill(0x7F)
-        log("noalloc: Q6_K 151936x3584, M=8 (must be rejected)")
+        log(f"noalloc: Q6_K 151936x3584, M={big} (must be rejected)")
         h = (ctypes.c_void_p * 1)(dts[0].handle)
         o = (ctypes.c_void_p * 1)(dy.ptr)
-        assert qmv.hip_lib().qmv_device_matvec_group_noalloc_f32(h, 1, dx.ptr, 8, o, stream.handle) == 0
+        assert qmv.hip_lib().qmv_device_matvec_group_noalloc_f32(h, 1, dx.ptr, big, o, stream.handle) == 0
         assert "scratch" in qmv.last_error()
         stream.synchronize()
-        assert np.all(dy.to_array(np.uint8, (4 * 8 * rows,)) == 0x7F)
+        assert np.all(dy.to_array(np.uint8, (4 * big * rows,)) == 0x7F)
         dts[0].close()
 
 
