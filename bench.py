@@ -182,12 +182,22 @@ def cpu_variants(qmv, host_layer, batch, seconds):
     return out
 
 
-def kernel_name(fmt, M):
-    """The kernel a Q4_K / Q6_K launch of M positions runs (default tuning)."""
+# Single-position Q4_K launches of at most this many (64-row tile, 256-weight
+# unit) pairs run on the row-major kernel (the library's policy, including its
+# QMV_ROWDOT / QMV_ROWDOT_ROWS switches read at start-up).
+ROWDOT_MAX_UNITS = 2048
+
+
+def kernel_name(fmt, M, tiled_units=None):
+    """The kernel a Q4_K / Q6_K launch of M positions over `tiled_units`
+    (tile, unit) pairs runs (default tuning)."""
     if M > 8:
         return "prefill_kernel<%s,%d>" % (fmt, 1 if M <= 16 else 2)
     if M >= (7 if fmt == "Q4_K" else 8):
         return "matvec_mfma_kernel<%s,%d>" % (fmt, M)
+    if (fmt == "Q4_K" and M == 1 and tiled_units is not None and tiled_units <= ROWDOT_MAX_UNITS
+            and os.environ.get("QMV_ROWDOT", "1") != "0"):
+        return "rowdot_q4k_kernel<%s,1,0>" % os.environ.get("QMV_ROWDOT_ROWS", "2")
     return "matvec_kernel<%s,%d>" % (fmt, M)
 
 
@@ -213,11 +223,15 @@ def build_launches(lib, layers, acts, outs, M):
             w = sum(T[n].packed_bytes for n in names)
             return w + 4 * M * cols + 4 * M * sum(T[n].rows for n in names)
 
-        kq, k6 = kernel_name("Q4_K", M), kernel_name("Q6_K", M)
-        launches.append((kq, algo(["q", "k", "v"], HIDDEN), grp(["q", "k", "v"], A["attn"])))
-        launches.append((kq, algo(["o"], HIDDEN), one("o", A["o"])))
-        launches.append((kq, algo(["gate", "up"], HIDDEN), grp(["gate", "up"], A["ffn"])))
-        launches.append((k6, algo(["down"], INTER), one("down", A["down"])))
+        def kern(fmt, names, cols):
+            return kernel_name(fmt, M, sum(-(-T[n].rows // 64) * (cols // 256) for n in names))
+
+        launches.append((kern("Q4_K", ["q", "k", "v"], HIDDEN), algo(["q", "k", "v"], HIDDEN),
+                         grp(["q", "k", "v"], A["attn"])))
+        launches.append((kern("Q4_K", ["o"], HIDDEN), algo(["o"], HIDDEN), one("o", A["o"])))
+        launches.append((kern("Q4_K", ["gate", "up"], HIDDEN), algo(["gate", "up"], HIDDEN),
+                         grp(["gate", "up"], A["ffn"])))
+        launches.append((kern("Q6_K", ["down"], INTER), algo(["down"], INTER), one("down", A["down"])))
     return launches
 
 
