@@ -141,7 +141,10 @@ int qmv_device_tensor_create(const QmvTensorView *matrix,
                              qmv_device_tensor *out_tensor);
 void qmv_device_tensor_destroy(qmv_device_tensor tensor);
 
-/* Shape and storage of a device tensor; any output pointer may be NULL. */
+/* Shape and storage of a device tensor; any output pointer may be NULL.
+ * device_bytes counts every device copy: the tiled layout, plus the GGUF
+ * bytes that small Q4_K tensors keep for the row-major single-position
+ * kernel. */
 int qmv_device_tensor_info(qmv_device_tensor tensor, int *rows, int *columns,
                            uint32_t *ggml_type, uint64_t *packed_bytes,
                            uint64_t *device_bytes);
