@@ -1574,6 +1574,114 @@ __device__ __forceinline__ void q6k_unit_mfma(const uint8_t *slab, const float *
     }
 }
 
+/* Q6_K at M <= 8 with two sub-blocks per 16x16x32 MFMA. A batch of at most 8
+ * positions leaves A rows 8..15 free, and a K = 32 MFMA costs the issue time
+ * of a K = 16 one on gfx950 (measured), so sub-blocks j = 8G + 2r + hf
+ * (r = 0, 1) and j + 4 (r + 2) run together: A rows 0..7 hold sub-block j's
+ * activations of positions 0..7 in k 0..15 and zeros in k 16..31, rows 8..15
+ * zeros in k 0..15 and sub-block j + 4's in k 16..31; B holds j's codes in k
+ * 0..15 and j + 4's in k 16..31. So D rows 0..7 are j's sums and rows 8..15
+ * j + 4's, each scaled by its own sub-block scale: half the MFMAs and half the
+ * scale FMAs of one K = 16 step per sub-block. Both sub-blocks take their
+ * codes from the same bytes: the ql plane's low (j) and high (j + 4) nibbles
+ * and the qh plane's bit pairs 2r and 2r + 4. Lane (kc, n): kc < 2 carries
+ * sub-block j, kc >= 2 sub-block j + 4, weights 8 (kc & 1) .. + 7 of it; its A
+ * values are zero unless n < 8 matches kc < 2. D[i][n] lands in lane
+ * n + 16 (i / 4), so lanes 32..63 hold the j + 4 sums of the positions that
+ * lanes 0..31 hold for j; the two halves are added once per work item, so acc
+ * must be zero on entry (the kernel runs one work item per wave). */
+template <int M, int PR0, int NPR>
+__device__ __forceinline__ void q6k_unit_mfma_pair(const uint8_t *slab, const float *xu, int ldx, int lane,
+                                                   f32x4_t (&acc)[4])
+{
+    static_assert(PR0 + NPR <= 4 && NPR >= 1 && M <= 8, "pairs of one unit, at most 8 positions");
+    constexpr int S0 = 2 * PR0, S1 = 2 * (PR0 + NPR); /* step s: pr = s >> 1, rr = s & 1 */
+    const int kc = lane >> 4, n = lane & 15;
+    const bool second = kc >= 2;
+    const bool carries = (n < 8) == !second;
+    const int pos = n < 8 ? n : n - 8;
+    /* Lanes of positions past the batch read position 0; those rows are never
+     * stored. Lanes that carry zeros read in bounds too. */
+    const float *xp = xu + (size_t)(pos < M ? pos : 0) * ldx + 8 * (kc & 1) + (second ? 64 : 0);
+    const uint8_t *wp = slab + n * 16 + 8 * (kc & 1); /* + plane * 1024 + g * 256 */
+    const int nsh = second ? 4 : 0;
+    uint4 sc[4];
+    float dg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        sc[g] = ld16(slab + 12 * 1024 + (16 * g + n) * 16);
+        dg[g] = f16_bits_to_f32(*(const unsigned short *)(slab + 13312 + (16 * g + n) * 2));
+    }
+    auto first_sub = [](int st) { return 8 * (st >> 2) + 2 * (st & 1) + ((st >> 1) & 1); };
+    auto ql_plane = [](int st) { return 4 * (st >> 2) + 2 * (st & 1) + ((st >> 1) & 1); };
+    auto qh_plane = [](int st) { return 8 + 2 * (st >> 2) + ((st >> 1) & 1); };
+    /* Codes of step s and s + 1 (ql and qh bytes, 8 of each per lane). */
+    uint2 ql[2][4], qh[2][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        ql[S0 & 1][g] = *(const uint2 *)(wp + ql_plane(S0) * 1024 + g * 256);
+        qh[S0 & 1][g] = *(const uint2 *)(wp + qh_plane(S0) * 1024 + g * 256);
+    }
+    float xv[2][8];
+    load_x<8>(xv[S0 & 1], (gf32 *)(xp + 16 * first_sub(S0)));
+#pragma unroll
+    for (int st = S0; st < S1; ++st) {
+        const int j = first_sub(st), rr = st & 1;
+        if (st + 1 < S1) {
+            load_x<8>(xv[(st + 1) & 1], ptr_after(xp + 16 * first_sub(st + 1), acc[0][0]));
+            gu8 *np = bytes_after(wp, acc[1][0]);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                ql[(st + 1) & 1][g] = gload8(np + ql_plane(st + 1) * 1024 + g * 256);
+                qh[(st + 1) & 1][g] = gload8(np + qh_plane(st + 1) * 1024 + g * 256);
+            }
+        }
+        bf16x8_t a0, a1, a2;
+        x_limbs<8>(xv[st & 1], carries, a0, a1, a2);
+        const int hsh = 2 * rr + (second ? 4 : 0);
+        f32x4_t d[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t l0 = (ql[st & 1][g].x >> nsh) & 0x0f0f0f0fu, l1 = (ql[st & 1][g].y >> nsh) & 0x0f0f0f0fu;
+            const uint32_t h0 = __builtin_amdgcn_perm(0u, 0x01008182u, (qh[st & 1][g].x >> hsh) & 0x03030303u);
+            const uint32_t h1 = __builtin_amdgcn_perm(0u, 0x01008182u, (qh[st & 1][g].y >> hsh) & 0x03030303u);
+            const bf16x2_t c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l0, 512.0f, false);
+            const bf16x2_t c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l0, 512.0f, true);
+            const bf16x2_t c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l1, 512.0f, false);
+            const bf16x2_t c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(l1, 512.0f, true);
+            const bf16x2_t e0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h0, 8192.0f, false);
+            const bf16x2_t e1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h0, 8192.0f, true);
+            const bf16x2_t e2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h1, 8192.0f, false);
+            const bf16x2_t e3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(h1, 8192.0f, true);
+            const bf16x8_t bl = {c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+            const bf16x8_t bh = {e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+            d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bl, d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bh, d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bl, d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bh, d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bl, d[g], 0, 0, 0);
+            d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, bh, d[g], 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            /* sub-block j's scale for lanes 0..31, j + 4's (the next scale
+             * word, same byte) for lanes 32..63 */
+            const uint32_t sw = second ? word(sc[g], (j >> 2) + 1) : word(sc[g], j >> 2);
+            const float sg = dg[g] * sbyte(sw, j & 3);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(sg, d[g][i], acc[g][i]);
+        }
+        /* One step's codes and scales live at a time (as for Q4_K). */
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    /* Lanes 0..31 add the sub-block j + 4 sums of their positions. */
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[g][i] += __shfl_xor(acc[g][i], 32, 64);
+}
+
 /* Part `part` of `parts` (1 or 2; wave-uniform) of one unit: consecutive
  * sub-blocks (Q4_K: 8 / parts, Q6_K: 16 / parts). */
 template <int FMT, int M>
@@ -1597,9 +1705,9 @@ __device__ __forceinline__ void unit_part_mfma(const uint8_t *slab, const float 
         else if (part == 0) q4k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
         else q4k_unit_mfma<M, 4, 4>(slab, xu, ldx, lane, acc);
     } else {
-        if (parts == 1) q6k_unit_mfma<M, 0, 4>(slab, xu, ldx, lane, acc);
-        else if (part == 0) q6k_unit_mfma<M, 0, 2>(slab, xu, ldx, lane, acc);
-        else q6k_unit_mfma<M, 2, 2>(slab, xu, ldx, lane, acc);
+        if (parts == 1) q6k_unit_mfma_pair<M, 0, 4>(slab, xu, ldx, lane, acc);
+        else if (part == 0) q6k_unit_mfma_pair<M, 0, 2>(slab, xu, ldx, lane, acc);
+        else q6k_unit_mfma_pair<M, 2, 2>(slab, xu, ldx, lane, acc);
     }
 }
 
