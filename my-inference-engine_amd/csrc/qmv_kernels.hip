@@ -2258,29 +2258,30 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
         prev = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(prev, 0));
         if (prev != (unsigned)S - 1u) return;
         asm volatile("" ::: "memory");
-        /* Eight positions x eight splits of loads in flight; each position
-         * is summed in split order, as sum_partials does. */
-        for (int m0 = 0; m0 < npos; m0 += 8) {
-            float sum[8];
-            for (int s0 = 0; s0 < S; s0 += 8) {
-                float v[8][8];
+        /* All MP position rows of 128 / MP splits in flight per round (the
+         * main loop's registers are free here), with no branch between the
+         * loads: rows past the batch and splits past the last read slots of
+         * this tile's workspace (in bounds) that are never used. Each
+         * position is summed in split order, as sum_partials does. */
+        constexpr int SB = 128 / MP;
+        float sum[MP];
+        for (int s0 = 0; s0 < S; s0 += SB) {
+            float v[SB][MP];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
+            for (int k = 0; k < SB; ++k) {
+                const float *pk = part + (size_t)min(s0 + k, S - 1) * MP * 64;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k)
-                        v[i][k] = m0 + i < npos && s0 + k < S
-                                      ? load_partial(part + ((size_t)(s0 + k) * MP + m0 + i) * 64)
-                                      : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-#pragma unroll
-                    for (int k = 0; k < 8; ++k)
-                        if (s0 + k < S) sum[i] = s0 + k == 0 ? v[i][k] : sum[i] + v[i][k];
+                for (int i = 0; i < MP; ++i) v[k][i] = load_partial(pk + i * 64);
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (m0 + i < npos) val[(m0 + i) * 64 + lane] = sum[i];
+            for (int k = 0; k < SB; ++k)
+                if (s0 + k < S)
+#pragma unroll
+                    for (int i = 0; i < MP; ++i) sum[i] = s0 + k == 0 ? v[k][i] : sum[i] + v[k][i];
         }
+#pragma unroll
+        for (int i = 0; i < MP; ++i)
+            if (i < npos) val[i * 64 + lane] = sum[i];
         if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     pf_emit<MP>(p, w, lane, val, npos);
