@@ -727,13 +727,23 @@ template <int M, int LOADS>
 __device__ __forceinline__ void sum_partials(const float *part, size_t stride, int n, float (&sum)[M])
 {
     constexpr int B = LOADS / M > 1 ? LOADS / M : 1;
+    /* With room for a pointer per split (LOADS >= 64), the loads carry no
+     * branch: splits past n repeat the last one (in bounds, not added). */
+    constexpr bool kClamp = LOADS >= 64;
     for (int b = 0; b < n; b += B) {
         float v[B][M];
 #pragma unroll
-        for (int i = 0; i < B; ++i)
+        for (int i = 0; i < B; ++i) {
+            if constexpr (kClamp) {
+                const float *pi = part + (size_t)min(b + i, n - 1) * stride;
 #pragma unroll
-            for (int m = 0; m < M; ++m)
-                v[i][m] = b + i < n ? load_partial(part + (size_t)(b + i) * stride + m * 64) : 0.0f;
+                for (int m = 0; m < M; ++m) v[i][m] = load_partial(pi + m * 64);
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                    v[i][m] = b + i < n ? load_partial(part + (size_t)(b + i) * stride + m * 64) : 0.0f;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < B; ++i)
             if (b + i < n)
