@@ -17,6 +17,10 @@
 #define QMV_MFMA_MAX_POSITIONS 32
 /* Tiles (one per wave) per prefill workgroup. */
 #define QMV_PF_TILES 4
+/* Floats of split-K workspace past the last partial: the VALU kernels' last
+ * split loads a batch of partials from one base pointer and may read up to
+ * this far beyond its tile's (discarding what it reads there). */
+#define QMV_PARTIAL_PAD 1024
 /* Words between the arrival counters of consecutive tiles: one counter per
  * 128-byte line, so the atomics of different tiles do not queue on a line. */
 #ifndef QMV_COUNTER_STRIDE

@@ -727,9 +727,12 @@ template <int M, int LOADS>
 __device__ __forceinline__ void sum_partials(const float *part, size_t stride, int n, float (&sum)[M])
 {
     constexpr int B = LOADS / M > 1 ? LOADS / M : 1;
-    /* With room for a pointer per split (LOADS >= 64), the loads carry no
-     * branch: splits past n repeat the last one (in bounds, not added). */
+    /* The loads carry no branch. With room for a pointer per split (LOADS >=
+     * 64), splits past n repeat the last one; otherwise they read on from one
+     * base pointer, up to B * stride <= QMV_PARTIAL_PAD floats past the
+     * tile's partials, which the workspace provides. Neither is added. */
     constexpr bool kClamp = LOADS >= 64;
+    static_assert(kClamp || B * M * 64 <= QMV_PARTIAL_PAD, "overread within the workspace padding");
     for (int b = 0; b < n; b += B) {
         float v[B][M];
 #pragma unroll
@@ -740,8 +743,7 @@ __device__ __forceinline__ void sum_partials(const float *part, size_t stride, i
                 for (int m = 0; m < M; ++m) v[i][m] = load_partial(pi + m * 64);
             } else {
 #pragma unroll
-                for (int m = 0; m < M; ++m)
-                    v[i][m] = b + i < n ? load_partial(part + (size_t)(b + i) * stride + m * 64) : 0.0f;
+                for (int m = 0; m < M; ++m) v[i][m] = load_partial(part + (size_t)(b + i) * stride + m * 64);
             }
         }
 #pragma unroll

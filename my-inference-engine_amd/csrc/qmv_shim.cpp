@@ -854,7 +854,7 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
     cp->grid = (int)wg;
     cp->waves = paired ? 2 * plan.waves : plan.waves;
     cp->fmt = t0->geo.format;
-    cp->partials = partials;
+    cp->partials = partials ? partials + QMV_PARTIAL_PAD : 0; /* padding past the last partial */
     cp->counters = counters;
     return 1;
 }
