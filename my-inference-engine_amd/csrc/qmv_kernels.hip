@@ -723,16 +723,20 @@ __device__ __forceinline__ void store_partial(float *p, float v)
  * elements go out before any is waited for (about LOADS in flight: 16 keeps
  * the VALU kernels' registers, 64 fits the matrix-core kernel's), so the sums
  * cost ceil(n / batch) memory round trips rather than M times that. */
-template <int M, int LOADS>
+template <int M, int LOADS, bool kBatch = (M >= 2)>
 __device__ __forceinline__ void sum_partials(const float *part, size_t stride, int n, float (&sum)[M])
 {
     constexpr int B = LOADS / M > 1 ? LOADS / M : 1;
-    /* The loads carry no branch. With room for a pointer per split (LOADS >=
-     * 64), splits past n repeat the last one; otherwise they read on from one
-     * base pointer, up to B * stride <= QMV_PARTIAL_PAD floats past the
-     * tile's partials, which the workspace provides. Neither is added. */
+    /* For batches the loads carry no branch. With room for a pointer per
+     * split (LOADS >= 64), splits past n repeat the last one; otherwise they
+     * read on from one base pointer, up to B * stride <= QMV_PARTIAL_PAD
+     * floats past the tile's partials, which the workspace provides. Neither
+     * is added. At one position (kBatch false: M == 1, and the gate and up
+     * sums of the paired SwiGLU finish; splits rarely past 4) a condition
+     * per load keeps the memory traffic to the partials that exist. */
     constexpr bool kClamp = LOADS >= 64;
-    static_assert(kClamp || B * M * 64 <= QMV_PARTIAL_PAD, "overread within the workspace padding");
+    constexpr bool kOverread = !kClamp && kBatch;
+    static_assert(!kOverread || B * M * 64 <= QMV_PARTIAL_PAD, "overread within the workspace padding");
     for (int b = 0; b < n; b += B) {
         float v[B][M];
 #pragma unroll
@@ -741,9 +745,13 @@ __device__ __forceinline__ void sum_partials(const float *part, size_t stride, i
                 const float *pi = part + (size_t)min(b + i, n - 1) * stride;
 #pragma unroll
                 for (int m = 0; m < M; ++m) v[i][m] = load_partial(pi + m * 64);
-            } else {
+            } else if constexpr (kOverread) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) v[i][m] = load_partial(part + (size_t)(b + i) * stride + m * 64);
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m)
+                    v[i][m] = b + i < n ? load_partial(part + (size_t)(b + i) * stride + m * 64) : 0.0f;
             }
         }
 #pragma unroll
@@ -1012,7 +1020,7 @@ __device__ __forceinline__ void finish_paired(const MatvecParams &p, const WgWor
         if (prev != (unsigned)S - 1u) return;
         asm volatile("" ::: "memory");
         float gu[2];
-        sum_partials<2, 16>(part, 128, S, gu);
+        sum_partials<2, 16, false>(part, 128, S, gu);
         g = gu[0];
         u = gu[1];
         if (lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
