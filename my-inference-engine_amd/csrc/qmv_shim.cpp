@@ -759,17 +759,8 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
      * tile in one workgroup, with no split-K tail: Q8_0 896 x 896 (7 units)
      * 4.80 us against 5.18-5.24 us in two splits. Longer rows keep the
      * splits (Q6_K 896 x 4864, 19 units: 6.1 us at 4 waves, 7.4 at 7). */
-    /* Single-position launches of 4097..16384 (tile, unit) pairs take eight
-     * waves: Qwen2.5-7B gate|up (2 x 18944 x 3584 Q4_K, 8288 pairs) runs in
-     * two splits of 8 and 6 units, 18.03 us against 18.67 in four splits of
-     * 4, 4, 4 and 2 (18.3 at five or seven waves). The fused SwiGLU keeps
-     * four, so that gate and up share a workgroup (finish_paired). */
     const bool one_split = batch == 1 && t0->units <= QMV_MAX_WAVES && total_tiles * t0->units <= 2048;
-    const long long pairs = total_tiles * t0->units;
-    const int short_waves = one_split                                  ? t0->units
-                            : batch == 1 && pairs > 16384              ? 5
-                            : batch == 1 && pairs > 4096 && !epi.swiglu ? QMV_MAX_WAVES
-                                                                       : 4;
+    const int short_waves = one_split ? t0->units : batch == 1 && total_tiles * t0->units > 16384 ? 5 : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
                                          mfma || parts > 1 ? 1 : 8);

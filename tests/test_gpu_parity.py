@@ -499,9 +499,9 @@ def test_device_api_matches_host_api(qmv, gpu, hip, t, rows, cols):
 @pytest.mark.parametrize("shapes", [[(3584, 31), (512, 32), (512, 33)], [(18944, 35), (18944, 36)]],
                          ids=["q|k|v", "gate|up"])
 def test_group_launch_matches_oracle(qmv, oracle, gpu, hip, shapes):
-    """q/k/v (row-major) and gate/up (tiled, 8288 (tile, unit) pairs: eight
-    waves per workgroup, splits of 8 and 6 units) sharing one input in one
-    launch: each within tolerance of the oracle."""
+    """q/k/v (row-major) and gate/up (tiled, 8288 (tile, unit) pairs in
+    splits of 4, 4, 4 and 2 units) sharing one input in one launch: each
+    within tolerance of the oracle."""
     cols = 3584
     raws = [qmv.synth_tensor(B.Q4_K, r, cols, seed=s) for r, s in shapes]
     dts = [qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, r, cols)) for raw, (r, _) in zip(raws, shapes)]
