@@ -16,12 +16,16 @@ of the tiled path:
     the greedy argmax of those logits;
   * repeated launches are bit-identical.
 """
+import os
+
 import numpy as np
 import pytest
 
 import _blocks as B
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(os.environ.get("QMV_ROWDOT", "1") == "0",
+                                 reason="the row-major kernel is switched off (QMV_ROWDOT=0)")]
 
 TOL = 1e-5
 SWIGLU_ULPS = 4
