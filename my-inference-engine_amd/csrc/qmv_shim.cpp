@@ -590,13 +590,16 @@ Plan plan_for(long long total_tiles, int units, int long_waves, int short_waves,
  * one wave per SIMD. Measured at M = 8 on the Qwen2.5-7B layer shapes (us per
  * launch, whole / half / quarter units): q|k|v (72 tiles x 14 units) 11.9 /
  * 10.8 / 12.4, o (56 x 14) 9.4 / 9.9 / 11.4, gate|up (592 x 14) 34.0 / 36.3 /
- * 50.8, down (56 x 74) 33.8 / 36.1 / 48.3. More items cost more split-K
- * partials than they gain, so quarters are not built. */
+ * 50.8, down (56 x 74) 33.8 / 36.1 / 48.3; Qwen2.5-1.5B gate|up (280 x 6,
+ * 1680 pairs) 13.4 / 12.9 (so the bound is 2048 pairs); with the current
+ * finish, quarters cost 7B q|k|v 10.4 against 9.8 and 1.5B down 11.3 against
+ * 9.75. More items cost more split-K partials than they gain, so quarters are
+ * not built. */
 int mfma_parts(int units, long long total_tiles)
 {
     const int forced = g_mfma_parts.load();
     if (forced == 1 || forced == 2) return forced;
-    return units < 32 && total_tiles * units <= 1024 ? 2 : 1;
+    return units < 32 && total_tiles * units <= 2048 ? 2 : 1;
 }
 
 /* Work items per K-unit on the VALU kernels for batches (M >= 2): halves.
