@@ -762,16 +762,21 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
      * tile in one workgroup, with no split-K tail: Q8_0 896 x 896 (7 units)
      * 4.80 us against 5.18-5.24 us in two splits. Longer rows keep the
      * splits (Q6_K 896 x 4864, 19 units: 6.1 us at 4 waves, 7.4 at 7). */
-    /* Matrix-core launches whose work items per tile divide by three take
-     * three waves (no idle wave, more workgroups): Qwen2.5-1.5B at M = 8,
-     * q|k|v (24 items) 7.47 us against 7.86 at four, o 7.18 against 7.55,
-     * gate|up (12) 12.24 against 12.7-13.1. Where three leaves idle waves
-     * four stays (Qwen2.5-7B q|k|v, 28 items: 10.8 against 9.9 us). */
+    /* Matrix-core launches take the waves per workgroup that leave no wave
+     * idle in a tile's last split: three if they divide the tile's work
+     * items, else four, else two. Measured at M = 8 (us per launch):
+     * Qwen2.5-1.5B q|k|v (24 items) 7.47 at three against 7.86 at four and
+     * 7.99 at two, o (24) 7.18 against 7.55, gate|up (12) 12.24 against
+     * 12.7-13.1 (12.2-12.3 at two); Qwen2.5-7B q|k|v (28) 9.9 at four
+     * against 10.8 at three and 10.2 at two, gate|up (14) 32.8-33.0 at two
+     * against 34.1 at four. */
+    const int items = t0->units * parts;
+    const int mfma_waves = items % 3 == 0 ? 3 : items % 4 == 0 ? 4 : items % 2 == 0 ? 2 : 4;
     const bool one_split = batch == 1 && t0->units <= QMV_MAX_WAVES && total_tiles * t0->units <= 2048;
-    const int short_waves = one_split                                 ? t0->units
+    const int short_waves = one_split                                       ? t0->units
                             : batch == 1 && total_tiles * t0->units > 16384 ? 5
-                            : mfma && (t0->units * parts) % 3 == 0    ? 3
-                                                                      : 4;
+                            : mfma                                          ? mfma_waves
+                                                                            : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
                                          mfma || parts > 1 ? 1 : 8);
