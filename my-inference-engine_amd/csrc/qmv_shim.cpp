@@ -549,8 +549,9 @@ struct Plan {
  * for long rows (>= 32 K-units) at M = 1, `long_waves` = 6: down 3584 x
  * 18944 Q6_K takes 14.4 us against 15.8 at 8 and 15.1 at 4, whose 19 splits
  * need two rounds of partial loads. Batches keep 4 for long rows too (down at
- * M = 8: 42.2 us against 45 at 8; 1536 x 8960 Q4_K at M = 2 and 4: 9-10%
- * faster than at 8). Many short workgroups keep every CU streaming until the
+ * M = 8: 42.2 us against 45 at 8 on the VALU path; 1536 x 8960 Q4_K at M = 2
+ * and 4: 9-10% faster than at 8), except Q6_K on the matrix cores, which
+ * takes 3 (plan_chunk). Many short workgroups keep every CU streaming until the
  * end and let the dispatcher balance the load; on MI355X this beat longer
  * waves and stream-K partitions at every decode shape measured. With
  * target_waves set, units per wave grow instead until about that many waves
@@ -769,8 +770,12 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
      * 7.99 at two, o (24) 7.18 against 7.55, gate|up (12) 12.24 against
      * 12.7-13.1 (12.2-12.3 at two); Qwen2.5-7B q|k|v (28) 9.9 at four
      * against 10.8 at three and 10.2 at two, gate|up (14) 32.8-33.0 at two
-     * against 34.1 at four. */
+     * against 34.1 at four. Long rows (32 units or more) on the matrix
+     * cores take three waves for Q6_K (7B down, 74 items: 29.6 us against
+     * 30.4 at four or two) and four for the other formats (1.5B Q4_K down,
+     * 35 items: 10.0 against 11.5 at three). */
     const int items = t0->units * parts;
+    const int long_batch_waves = mfma && t0->geo.format == QMV_FMT_Q6_K ? 3 : 4;
     const int mfma_waves = items % 3 == 0 ? 3 : items % 4 == 0 ? 4 : items % 2 == 0 ? 2 : 4;
     const bool one_split = batch == 1 && t0->units <= QMV_MAX_WAVES && total_tiles * t0->units <= 2048;
     const int short_waves = one_split                                       ? t0->units
@@ -778,7 +783,7 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
                             : mfma                                          ? mfma_waves
                                                                             : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
-                              : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : 4, short_waves,
+                              : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : long_batch_waves, short_waves,
                                          mfma || parts > 1 ? 1 : 8);
 
     qmv::MatvecParams &p = cp->p;
