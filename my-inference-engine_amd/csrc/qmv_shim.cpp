@@ -628,25 +628,25 @@ struct Epilogue {
 };
 
 /* Prefill launches (9..32 positions): a workgroup takes QMV_PF_TILES tiles
- * and a range of K-units. Measured on MI355X at Qwen2.5-7B layer shapes
- * (M = 32): five units per split for long rows (down, 74 units: 74 us
- * against 100 us at two) and for launches of many tile groups (gate|up, 148
- * groups: 64 us against 77 us at two); two for small launches (q|k|v, o:
- * 28 and 27 us against 41 at five), where more splits keep more CUs busy;
- * one for rows of at most 8 units in at most 8 tile groups (Q8_0 896 x 896:
- * 17.8 us against 19.3 at two for 32 positions, 11.2 against 12.8 for 16);
- * three for long rows in at most 8 tile groups (Qwen2.5-1.5B down 1536 x
- * 8960: 35.9 us against 38.1 at five for 32 positions, 23.3 against 26.6
- * for 16; the 7B down, 14 groups, takes 78.6 at three against 67 at five).
+ * and a range of K-units (units per split). Measured on MI355X at M = 32
+ * (us per launch, cold): rows of fewer than 32 units take one unit per split
+ * in at most 20 tile groups (Qwen2.5-7B q|k|v, 18 groups: 19.7 against 20.9
+ * at two; o 18.9 against 20.0; Qwen2.5-1.5B q|k|v 14.6 against 15.4, o 13.9
+ * against 15.1), five in 100 groups or more (7B gate|up, 148 groups: 48.8
+ * against 58.2 at three and 61.5 at four) and two in between (1.5B gate|up,
+ * 70 groups: 19.25 against 21.0 at one); long rows take two in at most 8
+ * tile groups (1.5B down 1536 x 8960: 23.0 against 24.7 at three) and five
+ * beyond (7B down, 14 groups: 52.7 against 57.3 at three). More splits keep
+ * more CUs busy until their partials cost more than they spread.
  * units_per_wave, when forced, sets the units per split instead. */
 Plan plan_prefill(long long groups, int units)
 {
     const int force_u = g_force_u.load();
-    int ups = force_u > 0                  ? force_u
-              : units >= 32 && groups <= 8   ? 3
-              : units >= 32 || groups >= 100 ? 5
-              : units <= 8 && groups <= 8    ? 1
-                                             : 2;
+    int ups = force_u > 0                ? force_u
+              : units >= 32              ? (groups <= 8 ? 2 : 5)
+              : groups >= 100            ? 5
+              : groups <= 20             ? 1
+                                         : 2;
     if (ups > units) ups = units;
     Plan p;
     p.units_per_wave = ups;
