@@ -763,9 +763,10 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
      * tile in one workgroup, with no split-K tail: Q8_0 896 x 896 (7 units)
      * 4.80 us against 5.18-5.24 us in two splits. Longer rows keep the
      * splits (Q6_K 896 x 4864, 19 units: 6.1 us at 4 waves, 7.4 at 7). */
-    /* Matrix-core launches take the waves per workgroup that leave no wave
-     * idle in a tile's last split: three if they divide the tile's work
-     * items, else four, else two. Measured at M = 8 (us per launch):
+    /* Matrix-core launches over rows of fewer than 32 units take the waves
+     * per workgroup that leave no wave idle in a tile's last split: three if
+     * three divides the tile's work items, else four if four does, else two
+     * if two does, else four. Measured at M = 8 (us per launch):
      * Qwen2.5-1.5B q|k|v (24 items) 7.47 at three against 7.86 at four and
      * 7.99 at two, o (24) 7.18 against 7.55, gate|up (12) 12.24 against
      * 12.7-13.1 (12.2-12.3 at two); Qwen2.5-7B q|k|v (28) 9.9 at four
