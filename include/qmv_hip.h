@@ -15,8 +15,10 @@
  *
  * Thread safety: all entry points may be called concurrently from several
  * host threads on the same registered weights (the reference's sessions do
- * this, include/engine_api.h:10-17). Host-pointer calls use a per-thread HIP
- * stream and per-thread staging buffers.
+ * this, include/engine_api.h:10-17). A host-pointer call checks a context (a
+ * HIP stream with its staging buffers and split-K workspace) out of a
+ * per-device pool for its duration; any thread may use any context, so a
+ * session may move between OS threads from call to call.
  */
 #ifndef QMV_HIP_H
 #define QMV_HIP_H
@@ -78,22 +80,37 @@ int qmv_tensor_matmul_f32(const QmvTensorView *matrix, const float *inputs,
  * Upload a packed tensor now (at model load) instead of on first use. No
  * reference counterpart: the reference reads weights straight from its mmap
  * (src/gguf_reader.cpp:695-697). Registration alone does not size the
- * per-thread staging or the split-K workspace; qmv_reserve_calls does.
+ * staging or the split-K workspace of the host-pointer calls;
+ * qmv_reserve_calls does.
  */
 int qmv_register_tensor(const QmvTensorView *matrix);
 
 /*
  * Register the tensor and pre-size, for host-pointer matvec/matmul calls on
- * it with 1..max_batch positions from the calling thread, everything those
- * calls would otherwise allocate on first use: the thread's HIP stream, its
- * pinned and device staging, and the stream's split-K workspace. Called for
- * every weight from the engine's state initialisation
- * (inference_state_init), it makes the reference's contracts hold: a forward
- * pass allocates nothing after init (include/engine.h:84-85) and the matvec
- * itself allocates nothing (src/quantized_matvec.h:24). A later change of the
- * launch tuning, another thread or a larger batch may allocate again.
+ * it with 1..max_batch positions, everything those calls would otherwise
+ * allocate on first use: the input and output staging (pinned and device) and
+ * the split-K workspace, in every context of the current device's pool (one
+ * is created if the pool has none). Called for every weight from the engine's
+ * state initialisation (inference_state_init), it makes the reference's
+ * contracts hold on whatever OS thread later runs the session: a forward pass
+ * allocates nothing after init (include/engine.h:84-85) and the matvec itself
+ * allocates nothing (src/quantized_matvec.h:24). The first reservation closes
+ * the pool: from then on a host-pointer call that finds every context in use
+ * waits for one to be returned instead of creating another. A larger batch
+ * than reserved, or a later change of the launch tuning, may allocate again.
  */
 int qmv_reserve_calls(const QmvTensorView *matrix, int max_batch);
+
+/*
+ * Declare how many host-pointer calls may run at once on the current device
+ * (the engine's number of concurrent sessions, server/pool.go:150): the pool
+ * gets at least `count` contexts (1..1024), each sized like every
+ * qmv_reserve_calls so far and later, and is closed as above. Call it at
+ * state initialisation, before or after the qmv_reserve_calls calls. No
+ * reference counterpart (the reference opens an OpenMP team per call,
+ * src/quantized_matvec.cpp:152).
+ */
+int qmv_reserve_contexts(int count);
 
 /*
  * Number of device allocations, pinned host allocations and stream
@@ -307,7 +324,9 @@ int qmv_device_count(void);
  * positions and Q8_0 launches of 4 to 8 (QMV_Q5_MFMA_MIN_BATCH /
  * QMV_Q8_MFMA_MIN_BATCH in the environment; 0 turns them off). Defaults may also come from the
  * QMV_TARGET_WAVES / QMV_UNITS_PER_WAVE / QMV_WAVES_PER_GROUP /
- * QMV_MFMA_MIN_BATCH environment variables. Any setting stays within the row
+ * QMV_MFMA_MIN_BATCH environment variables. While target_waves,
+ * units_per_wave or waves_per_group is set, single-position Q4_K launches use
+ * the tiled plan too (not the row-major kernel). Any setting stays within the row
  * tolerance: the plan only changes the summation order, and a given plan
  * always sums in the same order.
  */

@@ -87,6 +87,7 @@ HIP_SIGNATURES = {
     "qmv_tensor_matmul_f32": (ctypes.c_int, [_view_p, _vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int]),
     "qmv_register_tensor": (ctypes.c_int, [_view_p]),
     "qmv_reserve_calls": (ctypes.c_int, [_view_p, ctypes.c_int]),
+    "qmv_reserve_contexts": (ctypes.c_int, [ctypes.c_int]),
     "qmv_allocation_count": (ctypes.c_ulonglong, []),
     "qmv_release_tensor": (ctypes.c_int, [_vp]),
     "qmv_release_all": (None, []),
@@ -227,9 +228,17 @@ def register_tensor(view: QmvTensorView) -> int:
 
 
 def reserve_calls(view: QmvTensorView, max_batch: int) -> None:
-    """Register the tensor and pre-size this thread's staging and workspace
-    for host calls of up to ``max_batch`` positions on it."""
+    """Register the tensor and pre-size every pooled host context's staging
+    and workspace for host calls of up to ``max_batch`` positions on it, from
+    any thread."""
     if not hip_lib().qmv_reserve_calls(ctypes.byref(view), max_batch):
+        raise QmvError(last_error())
+
+
+def reserve_contexts(count: int) -> None:
+    """Declare ``count`` concurrent host-pointer callers: the device's context
+    pool gets that many contexts, sized like the reservations, and is closed."""
+    if not hip_lib().qmv_reserve_contexts(count):
         raise QmvError(last_error())
 
 

@@ -9,9 +9,10 @@
  *    pointer, type, shape), guarded by a sampled content fingerprint, so each
  *    packed tensor is uploaded and re-tiled once (the reference reads the same
  *    bytes from its mmap on every call).
- *  - Per-thread HIP stream, pinned staging and device I/O buffers for the
- *    host-pointer entry points (sessions call concurrently); a per-stream
- *    workspace (split-K partials, arrival counters, argmax partials).
+ *  - A per-device pool of contexts (HIP stream, pinned staging, device I/O
+ *    buffers) that host-pointer calls check out for their duration, from
+ *    any thread (sessions call concurrently); a per-stream workspace
+ *    (split-K partials, arrival counters, argmax partials).
  *  - Launch planning: tiles of 64 rows x K-units spread over waves,
  *    workgroups and K-splits.
  */
@@ -27,6 +28,7 @@
 #include <memory>
 #include <mutex>
 #include <atomic>
+#include <condition_variable>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -264,56 +266,71 @@ Workspace &workspace_for(int device, hipStream_t stream)
     return *slot;
 }
 
-/* ---- per-thread context for the host-pointer entry points -------------------- */
+/* ---- pooled contexts for the host-pointer entry points --------------------------
+ * A host-pointer call checks a context out of its device's pool for the
+ * duration of the call: a non-blocking HIP stream with that stream's split-K
+ * workspace, pinned staging for the input and the output, and device buffers.
+ * Any thread may run on any context (a thread first tries the one it used
+ * last), so a session may move between threads, as the reference allows
+ * (include/engine_api.h:12-13). Until the first reservation
+ * (qmv_reserve_calls, qmv_reserve_contexts) a pool grows when every context
+ * is checked out. A reservation closes it: from then on a call that finds
+ * every context checked out waits for one instead of creating another, and
+ * every context holds at least the largest reservation's staging and
+ * workspace, so reserved calls allocate nothing on any thread. Contexts are
+ * never freed (HIP may already be torn down at process exit). */
+
+struct CtxPool;
 
 struct HostCtx {
     int device = -1;
+    CtxPool *pool = nullptr;
     hipStream_t stream = nullptr;
+    Workspace *ws = nullptr; /* the stream's split-K workspace */
     float *h_in = nullptr, *h_out = nullptr;
     size_t h_in_cap = 0, h_out_cap = 0;
     float *d_in = nullptr, *d_out = nullptr; /* d_out: dequantised rows, sampler results */
     size_t d_in_cap = 0, d_out_cap = 0;
+    bool busy = false; /* checked out; guarded by the pool's mutex */
 };
 
-/* Contexts are never freed (HIP may already be torn down at process exit);
- * a thread returns its context to a pool when it ends and new threads reuse it. */
-std::mutex g_pool_mu;
-std::vector<HostCtx *> g_pool;
-
-struct CtxHolder {
-    HostCtx *ctx = nullptr;
-    ~CtxHolder()
-    {
-        if (ctx) {
-            std::lock_guard<std::mutex> lock(g_pool_mu);
-            g_pool.push_back(ctx);
-        }
-    }
+/* What a context holds at least: input and output staging floats, split-K
+ * partial floats and counter words. */
+struct CtxSizes {
+    size_t nin = 0, nout = 0, partials = 0, counters = 0;
 };
-thread_local CtxHolder t_ctx;
 
-HostCtx *host_ctx()
+CtxSizes max_sizes(const CtxSizes &a, const CtxSizes &b)
 {
-    if (!t_ctx.ctx) {
-        std::lock_guard<std::mutex> lock(g_pool_mu);
-        if (!g_pool.empty()) {
-            t_ctx.ctx = g_pool.back();
-            g_pool.pop_back();
-        } else {
-            t_ctx.ctx = new HostCtx();
-        }
-    }
-    HostCtx *c = t_ctx.ctx;
-    const int dev = g_device.load();
-    if (!hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
-    if (c->device != dev) {
-        /* Fresh device: new stream and buffers (old ones stay with the old device). */
-        *c = HostCtx();
-        g_allocations.fetch_add(1);
-        if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
-        c->device = dev;
-    }
-    return c;
+    CtxSizes z;
+    z.nin = a.nin > b.nin ? a.nin : b.nin;
+    z.nout = a.nout > b.nout ? a.nout : b.nout;
+    z.partials = a.partials > b.partials ? a.partials : b.partials;
+    z.counters = a.counters > b.counters ? a.counters : b.counters;
+    return z;
+}
+
+struct CtxPool {
+    std::mutex mu;
+    std::condition_variable cv;
+    std::vector<HostCtx *> all;
+    bool closed = false; /* reserved: wait for a context rather than create one */
+    CtxSizes sizes;      /* every context of a closed pool holds at least these */
+};
+
+/* Contexts per device at most (a pool that was never reserved stops growing
+ * there and waits instead). */
+constexpr int kMaxContexts = 1024;
+
+std::mutex g_pools_mu;
+std::map<int, CtxPool *> g_pools; /* pools are never destroyed */
+
+CtxPool &pool_for(int device)
+{
+    std::lock_guard<std::mutex> lock(g_pools_mu);
+    CtxPool *&p = g_pools[device];
+    if (!p) p = new CtxPool();
+    return *p;
 }
 
 int grow_pinned(float **p, size_t *cap, size_t n)
@@ -337,6 +354,133 @@ int grow_device(float **p, size_t *cap, size_t n)
     const size_t m = n + n / 2 + 1024;
     HIP_TRY(counted_malloc((void **)p, m * sizeof(float)));
     *cap = m;
+    return 1;
+}
+
+/* Grow a checked-out context to hold z (nothing is allocated if it does). */
+int ctx_fit(HostCtx *c, const CtxSizes &z)
+{
+    if (!grow_pinned(&c->h_in, &c->h_in_cap, z.nin) || !grow_pinned(&c->h_out, &c->h_out_cap, z.nout) ||
+        !grow_device(&c->d_in, &c->d_in_cap, z.nin))
+        return 0;
+    std::lock_guard<std::mutex> lock(c->ws->mu);
+    return workspace_reserve(*c->ws, c->stream, z.partials, z.counters);
+}
+
+/* A new context on the current device, sized to z; added to the pool as
+ * checked out (busy) or idle. Called with the pool's mutex held, so that a
+ * reservation sees every context the pool will ever have when it closes it. */
+HostCtx *ctx_create_locked(CtxPool &pool, int device, const CtxSizes &z, bool busy)
+{
+    if ((int)pool.all.size() >= kMaxContexts) {
+        set_error("more than %d host contexts requested on device %d", kMaxContexts, device);
+        return nullptr;
+    }
+    std::unique_ptr<HostCtx> c(new HostCtx());
+    g_allocations.fetch_add(1);
+    if (!hip_ok(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
+    c->device = device;
+    c->pool = &pool;
+    c->ws = &workspace_for(device, c->stream);
+    if (!ctx_fit(c.get(), z)) return nullptr; /* the stream stays (contexts are never freed) */
+    c->busy = busy;
+    pool.all.push_back(c.get());
+    return c.release();
+}
+
+thread_local HostCtx *t_last_ctx = nullptr;
+
+/* Check a context of the selected device out of its pool (waits while a
+ * closed pool has none free). The device is made current. */
+HostCtx *ctx_acquire()
+{
+    const int dev = g_device.load();
+    if (!hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+    CtxPool &pool = pool_for(dev);
+    std::unique_lock<std::mutex> lock(pool.mu);
+    for (;;) {
+        HostCtx *pick = nullptr;
+        if (t_last_ctx != nullptr && t_last_ctx->pool == &pool && !t_last_ctx->busy) {
+            pick = t_last_ctx;
+        } else {
+            for (HostCtx *c : pool.all)
+                if (!c->busy) {
+                    pick = c;
+                    break;
+                }
+        }
+        if (pick != nullptr) {
+            pick->busy = true;
+            t_last_ctx = pick;
+            return pick;
+        }
+        if (!pool.closed && (int)pool.all.size() < kMaxContexts) break;
+        pool.cv.wait(lock);
+    }
+    HostCtx *c = ctx_create_locked(pool, dev, pool.sizes, true);
+    if (c != nullptr) t_last_ctx = c;
+    return c;
+}
+
+void ctx_release(HostCtx *c)
+{
+    {
+        std::lock_guard<std::mutex> lock(c->pool->mu);
+        c->busy = false;
+    }
+    /* Every waiter re-checks: a reservation waits for one particular context. */
+    c->pool->cv.notify_all();
+}
+
+/* A context checked out for one call. A call that ends early (failure) may
+ * leave work queued on the stream that still reads the staging buffers, so
+ * the stream is drained before the next caller gets the context. */
+class CtxLease {
+public:
+    CtxLease() : c(ctx_acquire()) {}
+    ~CtxLease()
+    {
+        if (c == nullptr) return;
+        if (!done) (void)hipStreamSynchronize(c->stream);
+        ctx_release(c);
+    }
+    CtxLease(const CtxLease &) = delete;
+    CtxLease &operator=(const CtxLease &) = delete;
+    HostCtx *const c;
+    bool done = false; /* the call drained its stream */
+};
+
+/* Close the selected device's pool, raise what every context holds to at
+ * least `need`, grow each existing context to that, and create contexts up to
+ * `count`. Waits for contexts that are checked out. */
+int pool_reserve(const CtxSizes &need, int count)
+{
+    const int dev = g_device.load();
+    HIP_TRY(hipSetDevice(dev));
+    CtxPool &pool = pool_for(dev);
+    std::vector<HostCtx *> existing;
+    CtxSizes z;
+    {
+        std::lock_guard<std::mutex> lock(pool.mu);
+        pool.closed = true;
+        pool.sizes = max_sizes(pool.sizes, need);
+        z = pool.sizes;
+        existing = pool.all;
+    }
+    for (HostCtx *c : existing) {
+        {
+            std::unique_lock<std::mutex> lock(pool.mu);
+            pool.cv.wait(lock, [c] { return !c->busy; });
+            c->busy = true;
+        }
+        const int ok = ctx_fit(c, z);
+        ctx_release(c);
+        if (!ok) return 0;
+    }
+    std::lock_guard<std::mutex> lock(pool.mu);
+    while ((int)pool.all.size() < count)
+        if (ctx_create_locked(pool, dev, z, false) == nullptr) return 0;
+    pool.cv.notify_all();
     return 1;
 }
 
@@ -681,6 +825,8 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
                  const Epilogue &epi, ChunkPlan *cp)
 {
     if (g_rowdot.load() == 0 || count > QMV_MAX_JOBS) return false;
+    /* A forced tiled plan (qmv_set_launch_tuning) applies to every launch. */
+    if (g_target_waves.load() > 0 || g_force_u.load() > 0 || g_force_w.load() > 0) return false;
     const QmvDeviceTensor *t0 = ts[0];
     long long units = 0;
     for (int i = 0; i < count; ++i) {
@@ -957,7 +1103,8 @@ int host_matmul(const QmvTensorView *m, const float *in, int in_count, int batch
 {
     Shape s;
     if (!matvec_args_ok(m, in, in_count, out, out_count, batch, &s)) return 0;
-    HostCtx *c = host_ctx();
+    CtxLease lease;
+    HostCtx *c = lease.c;
     if (!c) return 0;
     std::shared_ptr<QmvDeviceTensor> t = cached_tensor(m, s, c);
     if (!t) return 0;
@@ -978,12 +1125,12 @@ int host_matmul(const QmvTensorView *m, const float *in, int in_count, int batch
     } else {
         HIP_TRY(hipMemcpyAsync(c->d_in, c->h_in, nin * sizeof(float), hipMemcpyHostToDevice, c->stream));
     }
-    Workspace &ws = workspace_for(c->device, c->stream);
     QmvDeviceTensor *tp = t.get();
     float *hout = nullptr;
     HIP_TRY(hipHostGetDevicePointer((void **)&hout, c->h_out, 0));
-    if (!launch_group(&tp, 1, c->d_in, batch, &hout, c->stream, ws)) return 0;
+    if (!launch_group(&tp, 1, c->d_in, batch, &hout, c->stream, *c->ws)) return 0;
     HIP_TRY(hipStreamSynchronize(c->stream));
+    lease.done = true;
     int armed = g_fail_next.load();
     while (armed > 0 && !g_fail_next.compare_exchange_weak(armed, armed - 1)) {
     }
@@ -1015,16 +1162,17 @@ QMV_API int qmv_register_tensor(const QmvTensorView *matrix)
 {
     Shape s;
     if (!view_layout_ok(matrix, &s)) return 0;
-    HostCtx *c = host_ctx();
-    if (!c) return 0;
-    return cached_tensor(matrix, s, c) ? 1 : 0;
+    CtxLease lease;
+    if (!lease.c) return 0;
+    return cached_tensor(matrix, s, lease.c) ? 1 : 0;
 }
 
 /* Pre-size everything a host-pointer call on this tensor needs, for batches
- * of 1..max_batch positions: the upload, the calling thread's stream and
- * staging, and its stream's split-K workspace for every launch such a call
- * makes (launches carry at most QMV_MFMA_MAX_POSITIONS positions, and a
- * launch's needs depend only on its own position count). */
+ * of 1..max_batch positions, in every context of the device's pool: the
+ * upload, the input and output staging, and the split-K workspace of every
+ * launch such a call makes (launches carry at most QMV_MFMA_MAX_POSITIONS
+ * positions, and a launch's needs depend only on its own position count).
+ * The pool gets a context if it has none, and is closed. */
 QMV_API int qmv_reserve_calls(const QmvTensorView *matrix, int max_batch)
 {
     Shape s;
@@ -1033,30 +1181,39 @@ QMV_API int qmv_reserve_calls(const QmvTensorView *matrix, int max_batch)
         set_error("max_batch must be positive and its staging addressable");
         return 0;
     }
-    HostCtx *c = host_ctx();
-    if (!c) return 0;
-    std::shared_ptr<QmvDeviceTensor> t = cached_tensor(matrix, s, c);
-    if (!t) return 0;
-    const size_t nin = (size_t)max_batch * (size_t)s.cols, nout = (size_t)max_batch * (size_t)s.rows;
-    if (!grow_pinned(&c->h_in, &c->h_in_cap, nin) || !grow_pinned(&c->h_out, &c->h_out_cap, nout) ||
-        !grow_device(&c->d_in, &c->d_in_cap, nin))
-        return 0;
+    std::shared_ptr<QmvDeviceTensor> t;
+    {
+        CtxLease lease;
+        if (!lease.c) return 0;
+        t = cached_tensor(matrix, s, lease.c);
+        if (!t) return 0;
+    }
+    CtxSizes need;
+    need.nin = (size_t)max_batch * (size_t)s.cols;
+    need.nout = (size_t)max_batch * (size_t)s.rows;
     QmvDeviceTensor *tp = t.get();
-    float *out = c->d_in; /* planning only: no launch is made */
-    size_t need_p = 0, need_c = 0;
+    float dummy = 0.0f; /* planning only: no launch is made, nothing is dereferenced */
+    float *out = &dummy;
     const int widest = max_batch < QMV_MFMA_MAX_POSITIONS ? max_batch : QMV_MFMA_MAX_POSITIONS;
     for (int nb = 1; nb <= widest; ++nb) {
         if (nb > QMV_VALU_MAX_POSITIONS && !use_prefill(tp->geo.format, nb)) continue;
         ChunkPlan cp;
-        if (!plan_chunk(&tp, 1, c->d_in, 0, nb, &out, Epilogue(), &cp)) return 0;
-        if (cp.partials > need_p) need_p = cp.partials;
-        if (cp.counters > need_c) need_c = cp.counters;
+        if (!plan_chunk(&tp, 1, &dummy, 0, nb, &out, Epilogue(), &cp)) return 0;
+        if (cp.partials > need.partials) need.partials = cp.partials;
+        if (cp.counters > need.counters) need.counters = cp.counters;
     }
-    Workspace &ws = workspace_for(c->device, c->stream);
-    std::lock_guard<std::mutex> lock(ws.mu);
-    if (!workspace_reserve(ws, c->stream, need_p, need_c)) return 0;
-    HIP_TRY(hipStreamSynchronize(c->stream));
-    return 1;
+    return pool_reserve(need, 1);
+}
+
+/* Give the device's pool at least `count` contexts, each sized like the
+ * reservations so far (and grown by later ones), and close it. */
+QMV_API int qmv_reserve_contexts(int count)
+{
+    if (count <= 0 || count > kMaxContexts) {
+        set_error("context count must be in 1..%d", kMaxContexts);
+        return 0;
+    }
+    return pool_reserve(CtxSizes(), count);
 }
 
 QMV_API unsigned long long qmv_allocation_count(void)
@@ -1096,7 +1253,8 @@ QMV_API int qmv_dequantize_rows_f32(const QmvTensorView *matrix, int first_row, 
         set_error("row range outside the tensor");
         return 0;
     }
-    HostCtx *c = host_ctx();
+    CtxLease lease;
+    HostCtx *c = lease.c;
     if (!c) return 0;
     std::shared_ptr<QmvDeviceTensor> t = cached_tensor(matrix, s, c);
     if (!t) return 0;
@@ -1106,6 +1264,7 @@ QMV_API int qmv_dequantize_rows_f32(const QmvTensorView *matrix, int first_row, 
                                 c->stream));
     HIP_TRY(hipMemcpyAsync(output, c->d_out, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
+    lease.done = true;
     return 1;
 }
 
@@ -1162,7 +1321,8 @@ QMV_API int qmv_greedy_sample_f32(const float *logits, int vocab_size, int *toke
         set_error("invalid greedy sampler arguments");
         return 0;
     }
-    HostCtx *c = host_ctx();
+    CtxLease lease;
+    HostCtx *c = lease.c;
     if (!c) return 0;
     const size_t n = (size_t)vocab_size;
     if (!grow_device(&c->d_in, &c->d_in_cap, n) || !grow_device(&c->d_out, &c->d_out_cap, 2) ||
@@ -1173,6 +1333,7 @@ QMV_API int qmv_greedy_sample_f32(const float *logits, int vocab_size, int *toke
     if (!qmv_device_greedy_argmax_f32(c->d_in, vocab_size, d_res, c->stream)) return 0;
     HIP_TRY(hipMemcpyAsync(c->h_out, d_res, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
+    lease.done = true;
     int res[2];
     memcpy(res, c->h_out, sizeof res);
     if (res[1] != 1) {
@@ -1192,10 +1353,12 @@ QMV_API int qmv_device_tensor_create(const QmvTensorView *matrix, qmv_device_ten
     *out_tensor = nullptr;
     Shape s;
     if (!view_layout_ok(matrix, &s)) return 0;
-    HostCtx *c = host_ctx();
+    CtxLease lease;
+    HostCtx *c = lease.c;
     if (!c) return 0;
     QmvDeviceTensor *t = nullptr;
     if (!tensor_upload(matrix, s, c->device, c->stream, &t)) return 0;
+    lease.done = true; /* the upload synchronised its stream */
     *out_tensor = t;
     return 1;
 }

@@ -65,8 +65,8 @@ def test_two_calls_second_smaller(qmv, gpu, hip):
         log("noalloc: Q4_K q|k|v 3584x3584 + 2x512x3584, M=8")
         _run_both(qmv, hip, qkv, 8, seed=501, stream=stream)
         small = _tensors(qmv, B.Q4_K, [512, 512], 3584, seed=510)
-        log("noalloc: Q4_K 2x512x3584, M=1")
-        _run_both(qmv, hip, small, 1, seed=511, stream=stream)
+        log("noalloc: Q4_K 2x512x3584, M=2")
+        _run_both(qmv, hip, small, 2, seed=511, stream=stream)
         gate = _tensors(qmv, B.Q4_K, [18944], 3584, seed=520)
         log("noalloc: Q4_K 18944x3584, M=32")
         _run_both(qmv, hip, gate, 32, seed=521, stream=stream)
@@ -110,24 +110,31 @@ def test_vocab_shape_and_oversized_call(qmv, gpu, hip):
         dts[0].close()
 
 
-def test_graph_capture_and_replays(qmv, gpu, hip):
-    """The call captured into a graph (its counter clear is a kernel node)
-    replays to the eager bits, with eager work between replays."""
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 896, 4864, 1), (B.Q4_K, 3584, 3584, 8),
+                                               (B.Q4_K, 3584, 3584, 1)])
+def test_graph_capture_and_replays(qmv, gpu, hip, t, rows, cols, batch):
+    """The call captured into a graph replays to the eager bits, with eager
+    work between replays. Q6_K 896 x 4864 at one position (19 K-units in 5
+    splits per tile) and Q4_K 3584 x 3584 at 8 positions split K, so their
+    counters live in the scratch array and are cleared by a fill-kernel node;
+    Q4_K 3584 x 3584 at one position runs row-major with no split."""
     with hip.Stream() as stream:
-        dts = _tensors(qmv, B.Q4_K, [3584], 3584, seed=550)
-        x = qmv.synth_normal(3584, seed=551)
+        dts = _tensors(qmv, t, [rows], cols, seed=550 + batch)
+        x = qmv.synth_normal(batch * cols, seed=551)
         dx = hip.DeviceBuffer.from_array(x)
-        dy = hip.DeviceBuffer(4 * 3584)
-        eager = _run_both(qmv, hip, dts, 1, seed=551, stream=stream)[0]
+        dy = hip.DeviceBuffer(4 * batch * rows)
+        log(f"noalloc graph: {B.NAMES[t]} {rows}x{cols}, M={batch}")
+        eager = _run_both(qmv, hip, dts, batch, seed=551, stream=stream)[0]
         with hip.Graph(stream) as g:
             g.begin()
-            qmv.device_matvec_group_noalloc(dts, dx.ptr, 1, [dy.ptr], stream.handle)
+            qmv.device_matvec_group_noalloc(dts, dx.ptr, batch, [dy.ptr], stream.handle)
             g.end()
             for i in range(4):
                 dy.fill(0)
                 g.replay()
                 stream.synchronize()
-                assert np.array_equal(dy.to_array(np.float32, (3584,)).view(np.uint32), eager.view(np.uint32)), i
-                qmv.device_matvec_group_noalloc(dts, dx.ptr, 1, [dy.ptr], stream.handle)
+                got = dy.to_array(np.float32, (batch * rows,))
+                assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), i
+                qmv.device_matvec_group_noalloc(dts, dx.ptr, batch, [dy.ptr], stream.handle)
                 stream.synchronize()
         dts[0].close()
