@@ -197,7 +197,8 @@ def kernel_name(fmt, M, tiled_units=None):
         return "matvec_mfma_kernel<%s,%d>" % (fmt, M)
     if (fmt == "Q4_K" and M == 1 and tiled_units is not None and tiled_units <= ROWDOT_MAX_UNITS
             and os.environ.get("QMV_ROWDOT", "1") != "0"):
-        return "rowdot_q4k_kernel<%s,1,0>" % os.environ.get("QMV_ROWDOT_ROWS", "2")
+        rows = os.environ.get("QMV_ROWDOT_ROWS", "2")
+        return "rowgroup_q4k_kernel<%s,64,0,false>" % (rows if rows in ("1", "2", "4") else "2")
     return "matvec_kernel<%s,%d>" % (fmt, M)
 
 

@@ -112,6 +112,7 @@ HIP_SIGNATURES = {
     "qmv_device_matvec_argmax_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "qmv_device_embed_rows_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]),
     "qmv_set_launch_tuning": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qmv_set_rowmajor": (None, [ctypes.c_int, ctypes.c_int]),
     "qmv_device_matvec_add_group_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, ctypes.c_int,
                                                        ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int),
                                                        ctypes.POINTER(_vp), _vp]),
@@ -221,6 +222,12 @@ def set_launch_tuning(target_waves: int = 0, units_per_wave: int = 0, waves_per_
                       mfma_min_batch: int = 0) -> None:
     """Process-wide launch-plan override (0 = automatic); see qmv_hip.h."""
     hip_lib().qmv_set_launch_tuning(target_waves, units_per_wave, waves_per_group, mfma_min_batch)
+
+
+def set_rowmajor(enable: bool = True, rows: int = 2) -> None:
+    """Row-major kernel for small single-position Q4_K launches on/off (and
+    its GGUF copies for tensors uploaded afterwards); rows per row segment."""
+    hip_lib().qmv_set_rowmajor(1 if enable else 0, rows)
 
 
 def register_tensor(view: QmvTensorView) -> int:

@@ -87,7 +87,7 @@ struct MatvecParams {
 
 /* One tensor of a row-major single-position launch (Q4_K): `w` holds the
  * GGUF bytes of the tensor (row r at r * sb * 144), workgroups
- * [wg_begin, next job's wg_begin) take `rows_per_wg` rows each. */
+ * [wg_begin, next job's wg_begin) take consecutive rows. */
 struct RowdotJob {
     const uint8_t *w;
     float *y;
@@ -101,8 +101,9 @@ struct RowdotParams {
     int njobs;
     const float *x; /* K activations, shared by all jobs */
     int sb;         /* super-blocks per row */
-    /* Fused greedy argmax (QMV_ROWDOT_ARGMAX): one candidate tile per
-     * workgroup, as MatvecParams describes. */
+    /* Fused greedy argmax (QMV_ROWDOT_ARGMAX): candidate tiles as
+     * MatvecParams describes (one per wave, or per workgroup when rows span
+     * waves). */
     uint64_t *argmax_cand;
     unsigned *argmax_count;
     int *argmax_result;
@@ -119,11 +120,14 @@ inline size_t argmax_words(size_t tiles) { return tiles + (tiles + 63) / 64; }
 inline size_t argmax_counts(size_t tiles) { return (tiles + 63) / 64 + 1; }
 
 hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s);
-/* Row-major Q4_K launch at one position: `rows_per_wg` (2, 4 or 8) rows per
- * workgroup of `waves` waves, `items` (1 or 2) 16-byte items per lane,
- * epilogue `epi` (QMV_ROWDOT_*). */
-hipError_t launch_rowdot(const RowdotParams &p, int rows_per_wg, int items, int epi, int grid, int waves,
-                         hipStream_t s);
+/* Row-major Q4_K launch at one position, one 64-weight group per lane.
+ * Rows of at most 16 super-blocks: workgroups of QMV_ROWGROUP_WAVES waves
+ * sharing the activations in LDS, each wave taking `rows` (1, 2 or 4) rows
+ * per segment of `seg` lanes (16, 32 or 64), so rows * 64 / seg rows per
+ * wave. Longer rows (seg = 64): a row spans the workgroup's `waves` waves,
+ * `rows` rows per workgroup. */
+#define QMV_ROWGROUP_WAVES 4
+hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
 /* status (may be null): cleared to 0 if any id is outside [0, rows). */

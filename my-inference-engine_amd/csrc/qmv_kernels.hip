@@ -885,6 +885,20 @@ __device__ __forceinline__ void tile_argmax(const P &p, int tile, bool valid, in
     }
 }
 
+/* Index of the job that owns this workgroup (jobs own consecutive ranges of
+ * workgroups from their wg_begin). Every comparison is independent, so the
+ * kernel-argument loads go out together instead of as a chain of dependent
+ * loads, one per job passed. */
+template <typename P>
+__device__ __forceinline__ int job_of_block(const P &p)
+{
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < QMV_MAX_JOBS; ++i)
+        if (i < p.njobs && (int)blockIdx.x >= p.job[i].wg_begin) j = i;
+    return j;
+}
+
 /* The workgroup's place in a launch: job, tile, K-split, and this wave's
  * K-units [u_begin, u_end). */
 struct WgWork {
@@ -906,8 +920,7 @@ __device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave, int it
         w.u_end = min(w.u_begin + p.units_per_wave, split_end);
         return w;
     }
-    int j = 0;
-    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const int j = job_of_block(p);
     const MatvecJob &job = p.job[j];
     const int local = blockIdx.x - job.wg_begin;
     w.job = j;
@@ -2203,8 +2216,7 @@ __device__ __forceinline__ void q50_unit_pf(const uint8_t *slab, const uint8_t *
 __device__ __forceinline__ WgWork locate_pf(const MatvecParams &p, int wave)
 {
     WgWork w;
-    int j = 0;
-    while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    const int j = job_of_block(p);
     const MatvecJob &job = p.job[j];
     const int local = blockIdx.x - job.wg_begin;
     const int group = local / job.splits;
@@ -2677,142 +2689,234 @@ rms_norm_kernel(const float *x, const float *__restrict__ w, int n, float eps, f
  * each wave, then across the workgroup's waves in wave order, so results are
  * run-to-run identical. */
 
-/* Sum of v over the 64 lanes of a wave, identical in every lane: pairs, quads,
- * 8s and 16s with DPP, then the four 16-lane rows in a fixed order. Every lane
- * must be active. */
+/* v plus the value DPP control CTRL brings to each lane (all lanes active). */
 template <int CTRL>
 __device__ __forceinline__ float dpp_plus(float v)
 {
     return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-__device__ __forceinline__ float wave_total(float v)
+/* Accumulate the 4 low-nibble codes of dword dw (bytes 0..3) against
+ * xlo[0..3] into l and the 4 high-nibble codes (as 16q) against xhi[0..3]
+ * into h, in byte order, on sums scaled by 2^-24 (f16lo above). */
+__device__ __forceinline__ void q4_dword_mix2(uint32_t dw, const float *xlo, const float *xhi, float &l, float &h)
+{
+    const uint32_t s = dw >> 8;
+    const uint32_t le = dw & 0x000f000fu, lo = s & 0x000f000fu; /* bytes 0,2 | 1,3 */
+    const uint32_t he = dw & 0x00f000f0u, ho = s & 0x00f000f0u;
+    l = fmaf(f16lo(le), xlo[0], l);
+    l = fmaf(f16lo(lo), xlo[1], l);
+    l = fmaf(f16hi(le), xlo[2], l);
+    l = fmaf(f16hi(lo), xlo[3], l);
+    h = fmaf(f16lo(he), xhi[0], h);
+    h = fmaf(f16lo(ho), xhi[1], h);
+    h = fmaf(f16hi(he), xhi[2], h);
+    h = fmaf(f16hi(ho), xhi[3], h);
+}
+
+/* Sum of v over each SEG-lane segment of the wave (SEG = 16, 32 or 64), as a
+ * wave-uniform value per segment: DPP inside the 16-lane rows, then the rows
+ * of a segment by readlane in a fixed order. Every lane must be active. */
+template <int SEG>
+__device__ __forceinline__ void segment_totals(float v, float (&out)[64 / SEG])
 {
     v = dpp_plus<0xB1>(v);  /* quad_perm [1,0,3,2] */
     v = dpp_plus<0x4E>(v);  /* quad_perm [2,3,0,1] */
     v = dpp_plus<0x141>(v); /* row_half_mirror */
     v = dpp_plus<0x140>(v); /* row_mirror */
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    if constexpr (SEG == 64) {
+        out[0] = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    } else if constexpr (SEG == 32) {
+        out[0] = lane_value(v, 0) + lane_value(v, 16);
+        out[1] = lane_value(v, 32) + lane_value(v, 48);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) out[k] = lane_value(v, 16 * k);
+    }
 }
 
-/* EPI: QMV_ROWDOT_STORE (y = sum, plus `add` if set), QMV_ROWDOT_SWIGLU (jobs
- * 0 = gate and 1 = up over the same rows in every workgroup; job 0's y gets
- * up * silu(gate)), QMV_ROWDOT_ARGMAX (one job; y stored, then the greedy
- * argmax of y with each workgroup as one candidate tile). */
-template <int R, int J, int EPI>
-__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowdot_q4k_kernel(RowdotParams p)
+/* Row-major Q4_K matvec at one position, one 64-weight group per lane.
+ *
+ * Lane item i of a row is group g = i & 3 of super-block s = i >> 2: qs
+ * bytes 32g..32g+31 (two 16-byte loads), whose low nibbles are weights
+ * 64g + j of the super-block (sub-block 2g) and high nibbles 64g + 32 + j
+ * (sub-block 2g + 1), plus the super-block's 16-byte header, read by its 4
+ * lanes as one line. A row has 4 sb items; a lane keeps the 64 activations of
+ * its item in VGPRs, with their two half sums, for every row it takes.
+ *
+ * Two modes, chosen by the row length:
+ *  - Shared (sb <= 16, workgroups of QMV_ROWGROUP_WAVES waves): a row takes
+ *    one segment of SEG lanes (the smallest of 16, 32, 64 that holds its
+ *    items), so a wave holds P = 64 / SEG segments; each wave takes R rows
+ *    per segment (rows row0 + w * R * P + r * P + segment). The activation
+ *    vector is staged once per workgroup in LDS, each 64-float item padded
+ *    by 16 bytes so that the lanes' 128-bit reads are free of bank
+ *    conflicts, and every wave reads its items from there.
+ *  - Split (sb > 16, SEG = 64): a row spans the workgroup's waves, which read
+ *    their own activations and add their sums in LDS in wave order.
+ * Every weight load is issued before any arithmetic; in shared mode the
+ * activation loads go first, so waiting for them leaves the weight loads in
+ * flight.
+ *
+ * EPI: QMV_ROWDOT_STORE (y = sum, plus `add` if set), QMV_ROWDOT_SWIGLU
+ * (jobs 0 = gate and 1 = up over the same rows: row slots R..2R-1 are job 1's
+ * rows, and job 0's y gets up * silu(gate), so the fused result is that of
+ * the plain launches' sums bit for bit), QMV_ROWDOT_ARGMAX (one job; y
+ * stored, then the greedy argmax of y with one candidate tile per wave in
+ * shared mode, per workgroup in split mode). Lane i < R * P of a wave emits
+ * the wave's row i. Row sums run in a fixed order (DPP within 16 lanes, the
+ * 16-lane rows by readlane, waves through LDS in wave order), so repeated
+ * launches are bit-identical. */
+template <int R, int SEG, int EPI, bool SPLIT>
+__global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(RowdotParams p)
 {
-    constexpr int RS = EPI == QMV_ROWDOT_SWIGLU ? 2 * R : R; /* row slots: gate rows, then up rows */
+    static_assert(!SPLIT || SEG == 64, "rows that span waves take whole waves");
+    constexpr int P = 64 / SEG;
+    constexpr int RS = EPI == QMV_ROWDOT_SWIGLU ? 2 * R : R;
+    constexpr int XW = QMV_ROWGROUP_WAVES;
+    constexpr bool split = SPLIT;
     __shared__ float red[QMV_MAX_WAVES][RS];
+    __shared__ float4 xsh[split ? 1 : 64 * 17]; /* shared mode: 64 items x (16 + 1 pad) float4 */
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
     int j = 0;
-    if constexpr (EPI == QMV_ROWDOT_STORE)
-        while (j + 1 < p.njobs && (int)blockIdx.x >= p.job[j + 1].wg_begin) ++j;
+    if constexpr (EPI == QMV_ROWDOT_STORE) j = job_of_block(p);
     const RowdotJob &job = p.job[j];
-    const int row0 = ((int)blockIdx.x - job.wg_begin) * R;
-    const int items = p.sb * 8;
+    const int local = (int)blockIdx.x - job.wg_begin;
+    const int row0 = split ? local * R : (local * XW + wave) * (R * P);
+    const int seg = P > 1 ? lane / SEG : 0;
+    const int items = 4 * p.sb;
+    const int it0 = split ? wave * 64 + lane : (lane & (SEG - 1));
+    const bool ok = it0 < items;
+    /* Lanes past the row's items repeat its last item (in-bounds loads) and
+     * drop their sums before the reduction. */
+    const int it = min(it0, items - 1);
+    const int s = it >> 2, g = it & 3;
     const size_t row_bytes = (size_t)p.sb * 144;
 
-    float xv[J][32], xl[J], xh[J];
-    int qoff[J], hoff[J], gsel[J];
-    bool ok[J];
-    /* Lanes past the row's items repeat its last item (in-bounds loads, no
-     * branches) and drop their sums before the reduction. */
+    /* Shared mode: this thread's part of the activation vector (K / 4 <=
+     * 1024 float4, XS per thread). */
+    constexpr int XS = 16 / XW;
+    float4 xstage[XS];
+    const int nx4 = 64 * p.sb;
+    if constexpr (!split) {
+        /* Threads past the vector repeat its last float4 (no branch, so the
+         * wait for these loads leaves the weight loads below in flight). */
 #pragma unroll
-    for (int i = 0; i < J; ++i) {
-        const int it0 = tid + i * (int)blockDim.x;
-        ok[i] = it0 < items;
-        const int it = min(it0, items - 1);
-        const int s = it >> 3, pl = it & 7, g = pl >> 1, h = pl & 1;
-        gsel[i] = g;
-        qoff[i] = 144 * s + 16 + 16 * pl;
-        hoff[i] = 144 * s;
-        const int k0 = 256 * s + 64 * g + 16 * h;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float4 lo = *(const float4 *)(p.x + k0 + 4 * c);
-            const float4 hi = *(const float4 *)(p.x + k0 + 32 + 4 * c);
-            xv[i][4 * c] = lo.x; xv[i][4 * c + 1] = lo.y; xv[i][4 * c + 2] = lo.z; xv[i][4 * c + 3] = lo.w;
-            xv[i][16 + 4 * c] = hi.x; xv[i][17 + 4 * c] = hi.y; xv[i][18 + 4 * c] = hi.z; xv[i][19 + 4 * c] = hi.w;
-        }
-        float a = 0.0f, b = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            a += xv[i][e];
-            b += xv[i][16 + e];
-        }
-        xl[i] = a;
-        xh[i] = b;
+        for (int i = 0; i < XS; ++i) xstage[i] = ((const float4 *)p.x)[min(tid + 64 * XW * i, nx4 - 1)];
     }
 
-    uint4 q[RS][J], hd[RS][J];
+    const int qoff = 144 * s + 16 + 32 * g, hoff = 144 * s;
+    uint4 qa[RS], qb[RS], hd[RS];
 #pragma unroll
     for (int r = 0; r < RS; ++r) {
         const RowdotJob &jr = r < R ? job : p.job[1];
-        const uint8_t *base = jr.w + (size_t)min(row0 + r % R, jr.rows - 1) * row_bytes;
-#pragma unroll
-        for (int i = 0; i < J; ++i) {
-            q[r][i] = ld16(base + qoff[i]);
-            hd[r][i] = ld16(base + hoff[i]);
-        }
+        const uint8_t *base = jr.w + (size_t)min(row0 + (r % R) * P + seg, jr.rows - 1) * row_bytes;
+        qa[r] = ld16(base + qoff);
+        qb[r] = ld16(base + qoff + 16);
+        hd[r] = ld16(base + hoff);
     }
 
-    float tot[RS];
+    float xv[64];
+    if constexpr (split) {
+        const float *xs = p.x + 256 * s + 64 * g;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const float4 v = *(const float4 *)(xs + 4 * c);
+            xv[4 * c] = v.x;
+            xv[4 * c + 1] = v.y;
+            xv[4 * c + 2] = v.z;
+            xv[4 * c + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            const int e = min(tid + 64 * XW * i, nx4 - 1);
+            xsh[(e >> 4) * 17 + (e & 15)] = xstage[i];
+        }
+        __syncthreads();
+        const float4 *mine = xsh + it * 17;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const float4 v = mine[c];
+            xv[4 * c] = v.x;
+            xv[4 * c + 1] = v.y;
+            xv[4 * c + 2] = v.z;
+            xv[4 * c + 3] = v.w;
+        }
+    }
+    /* Every load is issued before any arithmetic waits for one. */
+    __builtin_amdgcn_sched_barrier(0);
+
+    float xq[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        float t = xv[16 * c];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) t += xv[16 * c + e];
+        xq[c] = t;
+    }
+    const float xl = xq[0] + xq[1], xh = xq[2] + xq[3];
+    /* Scale/min bytes of sub-blocks 2g, 2g + 1 (header dwords y = bytes
+     * 4..7, z = 8..11, w = 12..15 of the super-block): byte pair 2(g & 1)
+     * of the dwords; for g >= 2 the 6-bit values are assembled from w's
+     * nibbles and the top 2 bits of y (scales) or z (minimums). */
+    const int sh = (g & 1) * 16;
+    const int shyz = sh + (g >= 2 ? 2 : 0);
+    const uint32_t nib = g >= 2 ? 0x0f0fu : 0u;
+
+    float tot[RS][P];
 #pragma unroll
     for (int r = 0; r < RS; ++r) {
-        float acc = 0.0f;
+        /* low / high code sums scaled by 2^-24 (q4_dword_mix2) */
+        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
 #pragma unroll
-        for (int i = 0; i < J; ++i) {
-            /* low / high code sums scaled by 2^-24 (q4_dword_mix) */
-            float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+        for (int e = 0; e < 4; ++e)
+            q4_dword_mix2(word(qa[r], e), xv + 4 * e, xv + 32 + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                q4_dword_mix(word(q[r][i], e), xv[i] + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
-            const uint4 h = hd[r][i];
-            const bool upper = gsel[i] >= 2;
-            const uint32_t scw = upper ? (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u) : h.y & 0x3f3f3f3fu;
-            const uint32_t mw = upper ? ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u) : h.z & 0x3f3f3f3fu;
-            const int sh = (gsel[i] & 1) * 16;
-            const uint32_t scp = scw >> sh, mp = mw >> sh;
-            const float d24 = f16_bits_to_f32(h.x) * 16777216.0f, dmin = f16_bits_to_f32(h.x >> 16);
-            /* d * sc is exact (11 x 6 significant bits); the power-of-2
-             * factors (2^24, 1/16 for high codes used as 16q) are exact. */
-            float c = (d24 * ubyte(scp, 0)) * (l0 + l1);
-            c = fmaf(d24 * ubyte(scp, 1) * 0.0625f, h0 + h1, c);
-            c = fmaf(-(dmin * ubyte(mp, 0)), xl[i], c);
-            c = fmaf(-(dmin * ubyte(mp, 1)), xh[i], c);
-            if (ok[i]) acc = i == 0 ? c : acc + c;
-        }
-        tot[r] = wave_total(acc);
+        for (int e = 0; e < 4; ++e)
+            q4_dword_mix2(word(qb[r], e), xv + 16 + 4 * e, xv + 48 + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
+        const uint4 h = hd[r];
+        const uint32_t sc = (((h.w >> sh) & nib) | ((h.y >> shyz) & ~nib)) & 0x3f3fu;
+        const uint32_t mn = (((h.w >> (sh + 4)) & nib) | ((h.z >> shyz) & ~nib)) & 0x3f3fu;
+        const float d24 = f16_bits_to_f32(h.x) * 16777216.0f, dmin = f16_bits_to_f32(h.x >> 16);
+        /* d * 2^24 * (sc_a * L + sc_b * H / 16) - dmin * (m_a * xl + m_b * xh) */
+        float u = ubyte(sc, 0) * (l0 + l1);
+        u = fmaf(ubyte(sc, 1), (h0 + h1) * 0.0625f, u);
+        float v = ubyte(mn, 0) * xl;
+        v = fmaf(ubyte(mn, 1), xh, v);
+        float c = d24 * u;
+        c = fmaf(-dmin, v, c);
+        segment_totals<SEG>(ok ? c : 0.0f, tot[r]);
     }
 
-    if (nw > 1) {
+    if constexpr (split) {
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < RS; ++r) red[wave][r] = tot[r];
+            for (int r = 0; r < RS; ++r) red[wave][r] = tot[r][0];
         }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int r = 0; r < RS; ++r) {
-            float s = red[0][r];
-            for (int v = 1; v < nw; ++v) s += red[v][r];
-            tot[r] = s;
+            float t = red[0][r];
+            for (int w = 1; w < nw; ++w) t += red[w][r];
+            tot[r][0] = t;
         }
     }
-    /* Lane r < R emits row row0 + r. */
-    float out = tot[0];
+    /* Lane i = r * P + segment emits row row0 + i. */
+    float out = tot[0][0], up = tot[RS > R ? R : 0][0];
 #pragma unroll
-    for (int r = 1; r < R; ++r)
-        if (lane == r) out = tot[r];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+            if (lane == r * P + q) {
+                out = tot[r][q];
+                if constexpr (EPI == QMV_ROWDOT_SWIGLU) up = tot[R + r][q];
+            }
     const int row = row0 + lane;
-    const bool valid = lane < R && row < job.rows;
+    const bool valid = lane < R * P && row < job.rows;
     if constexpr (EPI == QMV_ROWDOT_SWIGLU) {
-        float up = tot[R];
-#pragma unroll
-        for (int r = 1; r < R; ++r)
-            if (lane == r) up = tot[R + r];
         if (valid) {
             if (job.add != nullptr) out += job.add[row];
             if (p.job[1].add != nullptr) up += p.job[1].add[row];
@@ -2823,7 +2927,8 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowdot_q4k_kernel(RowdotPa
             if (job.add != nullptr) out += job.add[row];
             job.y[row] = out;
         }
-        if constexpr (EPI == QMV_ROWDOT_ARGMAX) tile_argmax(p, (int)blockIdx.x, valid, row, out, lane);
+        if constexpr (EPI == QMV_ROWDOT_ARGMAX)
+            tile_argmax(p, split ? (int)blockIdx.x : (int)blockIdx.x * XW + wave, valid, row, out, lane);
     }
 }
 
@@ -2872,21 +2977,24 @@ hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int wa
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_rowdot(const RowdotParams &p, int rows_per_wg, int items, int epi, int grid, int waves,
-                         hipStream_t s)
+hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s)
 {
-    if (waves < 1 || waves > QMV_MAX_WAVES || grid < 1) return hipErrorInvalidValue;
-#define QMV_ROWDOT(R, J, E)                                                                            \
-    if (rows_per_wg == R && items == J && epi == E) {                                                  \
-        hipLaunchKernelGGL((rowdot_q4k_kernel<R, J, E>), dim3(grid), dim3(waves * 64), 0, s, p);       \
+    if (waves < 1 || waves > QMV_MAX_WAVES || grid < 1 || (p.sb <= 16 && waves != QMV_ROWGROUP_WAVES) ||
+        (p.sb > 16 && seg != 64))
+        return hipErrorInvalidValue;
+    const bool split = p.sb > 16;
+#define QMV_ROWGROUP(R, SEG, E, SP)                                                                    \
+    if (rows == R && seg == SEG && epi == E && split == SP) {                                          \
+        hipLaunchKernelGGL((rowgroup_q4k_kernel<R, SEG, E, SP>), dim3(grid), dim3(waves * 64), 0, s, p); \
         return hipGetLastError();                                                                      \
     }
-#define QMV_ROWDOT_E(R, J) QMV_ROWDOT(R, J, QMV_ROWDOT_STORE) QMV_ROWDOT(R, J, QMV_ROWDOT_SWIGLU)           \
-    QMV_ROWDOT(R, J, QMV_ROWDOT_ARGMAX)
-    QMV_ROWDOT_E(2, 1) QMV_ROWDOT_E(4, 1) QMV_ROWDOT_E(8, 1) QMV_ROWDOT_E(2, 2) QMV_ROWDOT_E(4, 2)
-    QMV_ROWDOT_E(8, 2)
-#undef QMV_ROWDOT_E
-#undef QMV_ROWDOT
+#define QMV_ROWGROUP_E(R, SEG, SP) QMV_ROWGROUP(R, SEG, QMV_ROWDOT_STORE, SP)                         \
+    QMV_ROWGROUP(R, SEG, QMV_ROWDOT_SWIGLU, SP) QMV_ROWGROUP(R, SEG, QMV_ROWDOT_ARGMAX, SP)
+    QMV_ROWGROUP_E(1, 64, false) QMV_ROWGROUP_E(2, 64, false) QMV_ROWGROUP_E(4, 64, false)
+    QMV_ROWGROUP_E(2, 32, false) QMV_ROWGROUP_E(2, 16, false)
+    QMV_ROWGROUP_E(1, 64, true) QMV_ROWGROUP_E(2, 64, true) QMV_ROWGROUP_E(4, 64, true)
+#undef QMV_ROWGROUP_E
+#undef QMV_ROWGROUP
     return hipErrorInvalidValue;
 }
 

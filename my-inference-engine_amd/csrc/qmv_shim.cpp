@@ -492,19 +492,23 @@ int env_int(const char *name, int dflt)
 }
 
 /* Row-major single-position kernel for small Q4_K launches
- * (rowdot_q4k_kernel): QMV_ROWDOT = 0 turns it off (read at start-up, before
- * tensors are uploaded); QMV_ROWDOT_ROWS = rows per workgroup (2, 4 or 8).
- * Measured on MI355X in a graph of the Qwen2.5-7B decode set, us per launch
- * (tiled / rows per workgroup 2, 4, 8): q|k|v 6.81 / 6.11, 6.74, 7.73; o
- * 5.80 / 5.10, 5.49, 7.02; gate|up 18.5 / 26.4, 23.6, 23.1. Every workgroup
- * reads the row's whole activation vector, so the kernel pays only where the
- * tiled plan would split K across workgroups to fill the chip at all. */
+ * (rowgroup_q4k_kernel). QMV_ROWDOT = 0 turns it off at start-up and
+ * qmv_set_rowmajor at run time (tensors uploaded while it is off keep no
+ * GGUF copy); QMV_ROWDOT_ROWS / qmv_set_rowmajor set the rows a 64-lane row
+ * segment takes (1, 2 or 4; shorter rows' segments take 2). Measured on
+ * MI355X in a graph of the Qwen2.5-7B decode set, us per launch, q|k|v / o:
+ * tiled 6.81 / 5.80; workgroups of 4 waves sharing the activations in LDS,
+ * 1, 2 or 4 rows per wave: 4.85 / 4.19, 4.87 / 4.08, 5.67 / 4.51 (2 rows
+ * and per-wave activation loads: 7.1 / 5.8; 2 rows with 1, 2 or 8 waves per
+ * workgroup: 5.6 / 4.7, 5.2 / 4.8, 5.8 / 4.0). The tiled plan would split K
+ * across workgroups to fill the chip with these launches; gate|up (8288
+ * pairs) has enough tiles and stays tiled. */
 std::atomic<int> g_rowdot{env_int("QMV_ROWDOT", 1)};
 std::atomic<int> g_rowdot_rows{env_int("QMV_ROWDOT_ROWS", 2)};
 
-/* Super-blocks per row the row-major kernel takes: 8 waves x 64 lanes x 2
- * items, 8 items per super-block. */
-constexpr int kRowdotMaxSb = QMV_MAX_WAVES * 64 * 2 / 8;
+/* Super-blocks per row the row-major kernel takes: 8 waves x 64 lanes, 4
+ * lanes per super-block. */
+constexpr int kRowdotMaxSb = QMV_MAX_WAVES * 64 / 4;
 /* Launches of at most this many tiled (64-row tile, K-unit) pairs, summed over
  * the launch's tensors, run row-major: Qwen2.5-7B q|k|v (1008) and o (784),
  * not gate|up (8288). */
@@ -809,8 +813,8 @@ Plan plan_prefill(long long groups, int units)
 struct ChunkPlan {
     qmv::MatvecParams p;
     qmv::RowdotParams rp;                  /* row-major launch (rowdot): its parameters */
-    bool rowdot = false;
-    int rd_rows = 0, rd_items = 0, rd_epi = 0; /* rows per workgroup, 16-byte items per lane, epilogue */
+    bool rowdot = false;                   /* rowgroup_q4k_kernel */
+    int rd_rows = 0, rd_seg = 0, rd_epi = 0; /* rows per segment, lanes per row segment, epilogue */
     bool prefill = false, paired = false;
     int mt = 1, grid = 0, waves = 0, fmt = 0;
     size_t partials = 0, counters = 0;     /* floats / words of split-K workspace */
@@ -819,7 +823,7 @@ struct ChunkPlan {
 };
 
 /* A single-position launch of Q4_K tensors on the row-major kernel: every
- * tensor keeps its GGUF bytes, rows fit 8 waves of 2 items per lane, and the
+ * tensor keeps its GGUF bytes, rows fit 8 waves of 16 super-blocks, and the
  * epilogue is at most an added vector. */
 bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
                  const Epilogue &epi, ChunkPlan *cp)
@@ -836,12 +840,17 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     if (units > kRowdotMaxUnits) return false;
     if (epi.swiglu && (count != 2 || ts[1]->rows != t0->rows)) return false; /* rejected by the tiled plan */
     if (epi.argmax && (count != 1 || b0 != 0)) return false;
-    const int sb = t0->blocks_per_row, items = 8 * sb;
+    const int sb = t0->blocks_per_row;
     if (sb > kRowdotMaxSb) return false;
-    const int per_lane = items <= QMV_MAX_WAVES * 64 ? 1 : 2;
-    const int waves = (items + 64 * per_lane - 1) / (64 * per_lane);
+    /* Rows of at most 16 super-blocks: a segment of 16, 32 or 64 lanes per
+     * row, QMV_ROWGROUP_WAVES waves sharing the activations; longer rows span
+     * ceil(sb / 16) waves. */
+    const int seg = sb <= 4 ? 16 : sb <= 8 ? 32 : 64;
+    const bool split = sb > 16;
+    const int waves = split ? (4 * sb + 63) / 64 : QMV_ROWGROUP_WAVES;
     const int want = g_rowdot_rows.load();
-    const int R = want == 2 || want == 8 ? want : 4;
+    const int R = seg < 64 ? 2 : want == 1 || want == 4 ? want : 2;
+    const int wg_rows = split ? R : QMV_ROWGROUP_WAVES * R * (64 / seg);
     qmv::RowdotParams &rp = cp->rp;
     memset(&rp, 0, sizeof rp);
     rp.njobs = count;
@@ -855,17 +864,20 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         j.rows = ts[i]->rows;
         j.wg_begin = (int)wg;
         if (epi.add && epi.add[i]) j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
-        if (!epi.swiglu || i == 0) wg += (ts[i]->rows + R - 1) / R; /* SwiGLU: both jobs in each workgroup */
+        if (!epi.swiglu || i == 0) wg += (ts[i]->rows + wg_rows - 1) / wg_rows; /* SwiGLU: both jobs in each workgroup */
     }
-    if (wg > INT_MAX) return false;
+    /* Fused argmax candidates: one per wave when a wave's rows are its own,
+     * else one per workgroup. */
+    const long long cand = split ? wg : wg * QMV_ROWGROUP_WAVES;
+    if (cand > INT_MAX) return false;
     memset(&cp->p, 0, sizeof cp->p);
     cp->rowdot = true;
     cp->rd_rows = R;
-    cp->rd_items = per_lane;
+    cp->rd_seg = seg;
     cp->rd_epi = epi.swiglu ? QMV_ROWDOT_SWIGLU : epi.argmax ? QMV_ROWDOT_ARGMAX : QMV_ROWDOT_STORE;
     if (epi.argmax) {
         rp.argmax_result = epi.argmax;
-        rp.argmax_tiles = (int)wg;
+        rp.argmax_tiles = (int)cand;
     }
     cp->prefill = cp->paired = false;
     cp->mt = 1;
@@ -874,7 +886,7 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     cp->fmt = t0->geo.format;
     cp->partials = cp->counters = 0;
     cp->pair_vals = cp->pair_count = 0;
-    cp->argmax_tiles = epi.argmax ? (size_t)wg : 0;
+    cp->argmax_tiles = epi.argmax ? (size_t)cand : 0;
     return true;
 }
 
@@ -1042,7 +1054,7 @@ void bind_workspace(ChunkPlan &cp, float *partials, unsigned *counters)
 int enqueue_chunk(const ChunkPlan &cp, hipStream_t stream)
 {
     if (cp.rowdot)
-        HIP_TRY(qmv::launch_rowdot(cp.rp, cp.rd_rows, cp.rd_items, cp.rd_epi, cp.grid, cp.waves, stream));
+        HIP_TRY(qmv::launch_rowgroup(cp.rp, cp.rd_rows, cp.rd_seg, cp.rd_epi, cp.grid, cp.waves, stream));
     else if (cp.prefill)
         HIP_TRY(qmv::launch_prefill(cp.fmt, cp.p, cp.mt, cp.grid, stream));
     else
@@ -1655,6 +1667,12 @@ QMV_API void qmv_set_launch_tuning(int target_waves, int units_per_wave, int wav
     g_target_waves.store(target_waves > 0 ? target_waves : 0);
     g_force_u.store(units_per_wave > 0 ? units_per_wave : 0);
     g_force_w.store(waves_per_group > 0 && waves_per_group <= QMV_MAX_WAVES ? waves_per_group : 0);
+}
+
+QMV_API void qmv_set_rowmajor(int enable, int rows)
+{
+    g_rowdot.store(enable != 0 ? 1 : 0);
+    g_rowdot_rows.store(rows == 1 || rows == 2 || rows == 4 ? rows : 2);
 }
 
 QMV_API void qmv_debug_fail_next_calls(int count)

@@ -3,9 +3,12 @@ through the C ABI.
 
 Q4_K tensors whose tiled plan covers at most 2048 (64-row tile, 256-weight
 unit) pairs keep their GGUF bytes on the device as well, and their
-single-position launches run row-major: a workgroup owns whole rows, lanes
-split K, and a row's sums are added inside the workgroup. The bars are those
-of the tiled path:
+single-position launches run row-major (rowgroup_q4k_kernel): a lane takes
+one 64-weight group of a super-block, a row's lanes form a segment of 16, 32
+or 64 lanes (rows of up to 16 super-blocks; the workgroup's 4 waves share the
+activations through LDS) or span several waves (longer rows), and a row's
+sums are added inside the workgroup. Every case runs with 1, 2 and 4 rows per
+row segment (qmv_set_rowmajor). The bars are those of the tiled path:
   * rows: |y - y_oracle| <= 1e-5 * sum_k |w_k x_k| (the reference's scalar
     row loop, src/quantized_matvec.cpp:152-158, restated by the oracle);
   * the addend: bit-identical to the plain launch's rows plus the addend;
@@ -14,7 +17,11 @@ of the tiled path:
     oracle's transformer_swiglu_f32;
   * fused argmax: logits bit-identical to the plain launch, index equal to
     the greedy argmax of those logits;
-  * repeated launches are bit-identical.
+  * repeated launches are bit-identical;
+  * ties and non-finite logits in the fused argmax follow the reference
+    sampler (src/sampler.cpp:29-51);
+  * with the row-major kernel switched off, new tensors keep no GGUF copy and
+    run tiled, within the same bar.
 """
 import os
 
@@ -40,6 +47,18 @@ def log(msg):
 def hip(qmv):
     import importlib
     return importlib.import_module("my-inference-engine_amd.hip_runtime")
+
+
+ROWS_PER_SEGMENT = [1, 2, 4]
+
+
+@pytest.fixture(params=ROWS_PER_SEGMENT)
+def seg_rows(request, qmv):
+    """Rows per row segment for the launches of one test; the default (2)
+    is restored afterwards."""
+    qmv.set_rowmajor(True, request.param)
+    yield request.param
+    qmv.set_rowmajor(True, 2)
 
 
 def _bits(a):
@@ -70,16 +89,18 @@ def _check(oracle, raw, rows, cols, x, y, what):
     return float(np.max(err / np.maximum(absdot, 1e-300)))
 
 
-# rows: odd counts (a workgroup's second row missing), one row, tile edges;
-# K: 1 super-block, a fraction of a wave (6), more than a wave (14, 35), eight
-# full waves (64), and two items per lane (65, 100, 128).
-SHAPES = [(1, 256), (2, 256), (3, 512), (63, 1536), (64, 1536), (65, 3584), (513, 3584), (3584, 3584),
-          (257, 35 * 256), (130, 64 * 256), (64, 65 * 256), (131, 100 * 256), (1, 128 * 256), (128, 128 * 256)]
+# rows: odd counts (workgroups with missing rows), one row, tile edges;
+# K in super-blocks: 16-lane segments (1, 2, 4), 32-lane segments (6, 8),
+# 64-lane segments (14, 16), rows spanning 2 to 8 waves (17, 35, 64, 65,
+# 100, 128).
+SHAPES = [(1, 256), (2, 256), (3, 512), (5, 4 * 256), (63, 1536), (64, 1536), (9, 8 * 256), (65, 3584),
+          (513, 3584), (3584, 3584), (70, 16 * 256), (33, 17 * 256), (257, 35 * 256), (130, 64 * 256),
+          (64, 65 * 256), (131, 100 * 256), (1, 128 * 256), (128, 128 * 256)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
-def test_rowmajor_matches_oracle(qmv, oracle, gpu, hip, rows, cols):
-    log(f"row-major Q4_K {rows}x{cols}")
+def test_rowmajor_matches_oracle(qmv, oracle, gpu, hip, rows, cols, seg_rows):
+    log(f"row-major Q4_K {rows}x{cols}, {seg_rows} rows per segment")
     raw, dt = _device(qmv, rows, cols, seed=700 + rows + cols // 256)
     assert _tiled_units(rows, cols) <= SMALL_UNITS
     x = qmv.synth_normal(cols, seed=701 + rows)
@@ -99,7 +120,7 @@ def test_rowmajor_matches_oracle(qmv, oracle, gpu, hip, rows, cols):
     dt.close()
 
 
-def test_rowmajor_group_of_unequal_rows(qmv, oracle, gpu, hip):
+def test_rowmajor_group_of_unequal_rows(qmv, oracle, gpu, hip, seg_rows):
     """q|k|v-shaped group (Qwen2.5-7B): three tensors of 3584, 512 and 512 rows
     over one input, one launch."""
     cols = 3584
@@ -121,7 +142,7 @@ def test_rowmajor_group_of_unequal_rows(qmv, oracle, gpu, hip):
         dt.close()
 
 
-def test_rowmajor_addend_bit_exact(qmv, oracle, gpu, hip):
+def test_rowmajor_addend_bit_exact(qmv, oracle, gpu, hip, seg_rows):
     cols = 1536
     specs = [(1536, 720), (256, 721), (255, 722)]
     tensors = [_device(qmv, r, cols, seed) for r, seed in specs]
@@ -144,8 +165,8 @@ def test_rowmajor_addend_bit_exact(qmv, oracle, gpu, hip):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 256), (65, 512), (896, 3584), (1000, 1536)])
-def test_rowmajor_swiglu(qmv, oracle, gpu, hip, rows, cols):
-    log(f"row-major SwiGLU {rows}x{cols}")
+def test_rowmajor_swiglu(qmv, oracle, gpu, hip, rows, cols, seg_rows):
+    log(f"row-major SwiGLU {rows}x{cols}, {seg_rows} rows per segment")
     raw_g, dg = _device(qmv, rows, cols, 730)
     raw_u, du = _device(qmv, rows, cols, 731)
     x = qmv.synth_normal(cols, seed=732)
@@ -170,8 +191,8 @@ def test_rowmajor_swiglu(qmv, oracle, gpu, hip, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 256), (7, 512), (1000, 3584), (4099, 1536)])
-def test_rowmajor_fused_argmax(qmv, oracle, gpu, hip, rows, cols):
-    log(f"row-major fused argmax {rows}x{cols}")
+def test_rowmajor_fused_argmax(qmv, oracle, gpu, hip, rows, cols, seg_rows):
+    log(f"row-major fused argmax {rows}x{cols}, {seg_rows} rows per segment")
     raw, dt = _device(qmv, rows, cols, 740 + rows)
     x = qmv.synth_normal(cols, seed=741)
     dx = hip.DeviceBuffer.from_array(x)
@@ -188,6 +209,67 @@ def test_rowmajor_fused_argmax(qmv, oracle, gpu, hip, rows, cols):
             token, finite = res.to_array(np.int32, (2,))
             assert finite == 1 and token == int(np.argmax(y)), (token, int(np.argmax(y)))
         _check(oracle, raw, rows, cols, x, y, "logits")
+    dt.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 3584), (1000, 1536), (70, 20 * 256)])
+def test_rowmajor_argmax_ties_and_non_finite(qmv, gpu, hip, rows, cols, seg_rows):
+    """All-zero input: every logit is 0, so the lowest id wins (token 0). A row
+    whose first super-block has an infinite scale d gives a non-finite
+    logit: token -1 and flag 0, the reference sampler's rejection."""
+    log(f"row-major argmax ties / inf {rows}x{cols}, {seg_rows} rows per segment")
+    raw = qmv.synth_tensor(B.Q4_K, rows, cols, seed=760)
+
+    def fused(buf, x):
+        dt = qmv.DeviceTensor(qmv.make_view(buf, B.Q4_K, rows, cols))
+        assert dt.device_bytes > -(-rows // 64) * (cols // 256) * 64 * 144  # keeps the row-major copy
+        dx = hip.DeviceBuffer.from_array(x)
+        logits = hip.DeviceBuffer(4 * rows)
+        res = hip.DeviceBuffer(8)
+        with hip.Stream() as s:
+            out = []
+            for _ in range(2):
+                qmv.device_matvec_argmax(dt, dx.ptr, logits.ptr, res.ptr, s.handle)
+                s.synchronize()
+                out.append(res.to_array(np.int32, (2,)).tolist())
+        y = logits.to_array(np.float32, (rows,))
+        dt.close()
+        return out, y
+
+    out, y = fused(raw, np.zeros(cols, dtype=np.float32))
+    assert out == [[0, 1]] * 2 and not y.any()
+    bad = raw.copy()
+    row = rows - 3
+    off = row * (cols // 256) * 144
+    bad[off:off + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), dtype=np.uint8)
+    out, y = fused(bad, qmv.synth_normal(cols, seed=761))
+    assert not np.isfinite(y[row]) and np.isfinite(np.delete(y, row)).all()
+    assert out == [[-1, 0]] * 2
+
+
+def test_rowmajor_switched_off(qmv, oracle, gpu, hip):
+    """qmv_set_rowmajor(0, .): a tensor uploaded afterwards keeps only the
+    tiled layout, and its launches (tiled) stay within the row bar; switched
+    back on, new tensors keep the copy again."""
+    rows, cols = 3584, 3584
+    raw = qmv.synth_tensor(B.Q4_K, rows, cols, seed=770)
+    x = qmv.synth_normal(cols, seed=771)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(4 * rows)
+    tiled = 56 * 14 * 64 * 144
+    qmv.set_rowmajor(False, 2)
+    try:
+        dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, rows, cols))
+        assert dt.device_bytes == tiled
+        with hip.Stream() as s:
+            dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+            s.synchronize()
+        _check(oracle, raw, rows, cols, x, dy.to_array(np.float32, (rows,)), "row-major off")
+        dt.close()
+    finally:
+        qmv.set_rowmajor(True, 2)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, rows, cols))
+    assert dt.device_bytes == tiled + rows * 14 * 144
     dt.close()
 
 
