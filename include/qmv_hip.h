@@ -311,11 +311,11 @@ int qmv_device_count(void);
  * range of K-units, processed by waves_per_group waves of units_per_wave
  * units each (default: 1 unit and 4 waves; for single-position launches 6
  * waves over rows of 32 or more K-units, 5 over more than 16384 units in all,
- * and one wave per unit with no K split over rows of at most 8 units in
- * launches of at most 2048 units; batches run half units, except on the
- * matrix cores over rows of 32
- * or more units); a tile's K is split across workgroups as far as that requires,
- * and the last split to finish adds the partials in split order.
+ * 2 over 2049..16384 units, and one wave per unit with no K split over rows
+ * of at most 8 units in launches of at most 2048 units; batches run half
+ * units, except on the matrix cores over rows of 32 or more units); a tile's
+ * K is split across workgroups as far as that requires, and the last split to
+ * finish adds the partials in split order.
  * target_waves, if set, instead grows the units per wave until about that
  * many waves cover the launch. Q4_K and Q6_K batches of at least
  * mfma_min_batch positions (default 7 for Q4_K, 8 for Q6_K; a value above

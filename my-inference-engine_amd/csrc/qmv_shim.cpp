@@ -917,6 +917,13 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
      * (three splits of 14 units instead of four) measured 80.9 us against
      * 84.8-86.8 at four for 151936 x 3584 Q6_K, while four stays best for
      * the decode-step launches (o 3584 x 3584: 6.0 against 6.6 us). */
+    /* Single-position launches of 2049..16384 units over rows of fewer than
+     * 32 units (Qwen2.5-7B gate|up: 592 tiles x 14 units) take two waves per
+     * workgroup, so a tile's 14 units fill 14 wave slots (7 splits) instead
+     * of 16 (four splits of 4, 4, 4 and 2): the launch then needs 8288 slots
+     * where 8192 fit at once, not 9472. gate|up 18.1-18.2 us against
+     * 18.65-19.05 at four waves (17.97 at eight, 18.2 at three), and the fused
+     * SwiGLU, paired in workgroups of 2 x 2 waves, 18.1 against 18.3-18.5. */
     /* Small single-position launches over rows of at most 8 units take each
      * tile in one workgroup, with no split-K tail: Q8_0 896 x 896 (7 units)
      * 4.80 us against 5.18-5.24 us in two splits. Longer rows keep the
@@ -940,6 +947,7 @@ int plan_chunk(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0,
     const int short_waves = one_split                                       ? t0->units
                             : batch == 1 && total_tiles * t0->units > 16384 ? 5
                             : mfma                                          ? mfma_waves
+                            : batch == 1 && total_tiles * t0->units > 2048  ? 2
                                                                             : 4;
     const Plan plan = prefill ? plan_prefill(total_groups, t0->units)
                               : plan_for(total_tiles, t0->units * parts, batch == 1 ? 6 : long_batch_waves, short_waves,
