@@ -203,10 +203,11 @@ def kernel_name(fmt, M, tiled_units=None):
 
 
 def build_launches(lib, layers, acts, outs, M):
-    """One step = 4 launches per layer, arguments prepared once."""
+    """One step = 4 launches per layer, arguments prepared once: (kernel name,
+    algorithmic bytes, callable(stream), launch shape)."""
     grp_fn = lib.qmv_device_matvec_group_f32
     one_fn = lib.qmv_device_matvec_f32
-    launches = []  # (kernel name, algorithmic bytes, callable(stream))
+    launches = []
     for layer in range(LAYERS):
         T, A, O = layers[layer], acts[layer], outs[layer]
 
@@ -228,11 +229,11 @@ def build_launches(lib, layers, acts, outs, M):
             return kernel_name(fmt, M, sum(-(-T[n].rows // 64) * (cols // 256) for n in names))
 
         launches.append((kern("Q4_K", ["q", "k", "v"], HIDDEN), algo(["q", "k", "v"], HIDDEN),
-                         grp(["q", "k", "v"], A["attn"])))
-        launches.append((kern("Q4_K", ["o"], HIDDEN), algo(["o"], HIDDEN), one("o", A["o"])))
+                         grp(["q", "k", "v"], A["attn"]), "qkv"))
+        launches.append((kern("Q4_K", ["o"], HIDDEN), algo(["o"], HIDDEN), one("o", A["o"]), "o"))
         launches.append((kern("Q4_K", ["gate", "up"], HIDDEN), algo(["gate", "up"], HIDDEN),
-                         grp(["gate", "up"], A["ffn"])))
-        launches.append((kern("Q6_K", ["down"], INTER), algo(["down"], INTER), one("down", A["down"])))
+                         grp(["gate", "up"], A["ffn"]), "gate_up"))
+        launches.append((kern("Q6_K", ["down"], INTER), algo(["down"], INTER), one("down", A["down"]), "down"))
     return launches
 
 
@@ -243,8 +244,8 @@ def run_set(qmv, hip, stream, launches, steps, warmup, use_graph):
     sp = stream.handle
 
     def step():
-        for _, _, fn in launches:
-            if fn(sp) != 1:
+        for launch in launches:
+            if launch[2](sp) != 1:
                 raise RuntimeError(qmv.last_error())
 
     for _ in range(max(1, warmup)):
@@ -285,16 +286,17 @@ def run_set(qmv, hip, stream, launches, steps, warmup, use_graph):
             "p90": q(0.9), "eager_ms": eager * 1e3 if eager else None, "graph": graph is not None}
 
 
-def launch_profile(hip, stream, launches, passes, use_graph):
-    """Average duration per launch of each kernel: the kernel's own launches
-    of one step, in step order, captured in a HIP graph and replayed `passes`
-    times between two HIP events on the launch stream (no event between
-    launches, so dispatch overhead is counted as in the timed replays).
-    Returns {kernel: [algorithmic bytes, ms, launches]} over all passes."""
+def launch_profile(hip, stream, launches, passes, use_graph, key=0):
+    """Average duration per launch of each kernel (key 0) or launch shape
+    (key 3): the group's own launches of one step, in step order, captured in
+    a HIP graph and replayed `passes` times between two HIP events on the
+    launch stream (no event between launches, so dispatch overhead is
+    counted as in the timed replays). Returns {group: [algorithmic bytes, ms,
+    launches]} over all passes."""
     per_kernel = {}
     sp = stream.handle
-    for name in sorted({n for n, _, _ in launches}):
-        mine = [(b, fn) for n, b, fn in launches if n == name]
+    for name in sorted({launch[key] for launch in launches}):
+        mine = [(launch[1], launch[2]) for launch in launches if launch[key] == name]
         run = lambda: [fn(sp) for _, fn in mine]
         graph = None
         if use_graph:
@@ -318,6 +320,30 @@ def launch_profile(hip, stream, launches, passes, use_graph):
         if graph is not None:
             graph.destroy()
     return per_kernel
+
+
+def streaming_floor(probe, hip, stream, launches, passes, main_run, no_graph):
+    """Streaming floors in the same run: each launch shape's launches of one
+    step (and the whole step) as dependent read-only launches over distinct
+    buffers of the same byte counts, replayed from a graph
+    (probe.read_chain_us), against the matvec launches of that shape timed
+    the same way (launch_profile by shape)."""
+    shapes = launch_profile(hip, stream, launches, passes, not no_graph, key=3)
+    out = {"method": "graph of dependent read-only launches over distinct buffers of each launch's "
+                     "algorithmic bytes, each read once (fastest of 1/2/4/8 loads in flight per thread), "
+                     "same run",
+           "floor_us": {}, "kernel_us": {}, "kernel_to_floor": {}}
+    for shape, (nbytes, ms, count) in shapes.items():
+        sizes = [launch[1] for launch in launches if launch[3] == shape]
+        floor = probe.read_chain_us(sizes) / len(sizes)
+        us = ms / count * 1e3
+        out["floor_us"][shape] = round(floor, 3)
+        out["kernel_us"][shape] = round(us, 3)
+        out["kernel_to_floor"][shape] = round(us / floor, 3)
+    set_floor = probe.read_chain_us([launch[1] for launch in launches]) / 1e3
+    out["set_floor_ms"] = round(set_floor, 4)
+    out["set_to_floor"] = round(main_run["ms_per_step"] / set_floor, 3)
+    return out
 
 
 def vocab_bench(qmv, hip, stream, reps):
@@ -602,6 +628,7 @@ def main():
             extra["decode_step_with_element_ops"] = ops
         extra["small_configs"] = small_configs_bench(qmv, hip, stream, max(5, args.steps // 10))
         probe = importlib.import_module("my-inference-engine_amd.probe")
+        extra["streaming_floor"] = streaming_floor(probe, hip, stream, launches, passes, main_run, args.no_graph)
         extra["hbm_read_probe"] = probe.read_bandwidth(1 << 30, 512, 10)
         extra["hbm_fraction_of_read_probe"] = round(value / extra["hbm_read_probe"]["gbs"], 4)
 

@@ -4,6 +4,9 @@ plain copy of known size for calibrating rocprofv3's FETCH_SIZE / WRITE_SIZE.
     python3 my-inference-engine_amd/probe.py read [--mib 1024] [--blocks 512]
     python3 my-inference-engine_amd/probe.py copy [--mib 512] [--reps 1]
 
+read_chain_us() (used by bench.py) gives the streaming floor of a sequence
+of launches.
+
 Each prints one JSON line. Measurement tooling only; the matvec path does not
 use it.
 """
@@ -28,6 +31,9 @@ def probe_lib() -> ctypes.CDLL:
                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]
         lib.qmv_probe_copy.restype = ctypes.c_int
         lib.qmv_probe_copy.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+        lib.qmv_probe_read_chain.restype = ctypes.c_int
+        lib.qmv_probe_read_chain.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
         _lib = lib
     return _lib
 
@@ -47,6 +53,21 @@ def copy_pass(nbytes: int = 512 << 20, reps: int = 1) -> dict:
         raise RuntimeError("qmv_probe_copy failed")
     return {"probe": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "reps": reps,
             "us_per_pass": round(ms.value * 1e3, 3), "gbs": round(2 * nbytes / (ms.value * 1e-3) / 1e9, 1)}
+
+
+def read_chain_us(sizes, reps: int = 20, pers=(1, 2, 4, 8)) -> float:
+    """Streaming floor of a launch sequence: microseconds per replay of a
+    graph of dependent read-only launches over distinct buffers of `sizes`
+    bytes, each read once by threads that issue `per` 16-byte loads at once
+    (the fastest of the `pers` tried)."""
+    arr = (ctypes.c_uint64 * len(sizes))(*sizes)
+    best = None
+    for per in pers:
+        us = ctypes.c_double()
+        if probe_lib().qmv_probe_read_chain(arr, len(sizes), per, reps, ctypes.byref(us)) != 1:
+            raise RuntimeError("qmv_probe_read_chain failed")
+        best = us.value if best is None else min(best, us.value)
+    return best
 
 
 def main():
