@@ -2778,6 +2778,8 @@ __device__ __forceinline__ void segment_totals(float v, float (&out)[64 / SEG])
  * the wave's row i. Row sums run in a fixed order (DPP within 16 lanes, the
  * 16-lane rows by readlane, waves through LDS in wave order), so repeated
  * launches are bit-identical. */
+typedef void __attribute__((address_space(3))) lds_void;
+
 template <int R, int SEG, int EPI, bool SPLIT>
 __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(RowdotParams p)
 {
@@ -2787,7 +2789,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     constexpr int XW = QMV_ROWGROUP_WAVES;
     constexpr bool split = SPLIT;
     __shared__ float red[QMV_MAX_WAVES][RS];
-    __shared__ float4 xsh[split ? 1 : 64 * 17]; /* shared mode: 64 items x (16 + 1 pad) float4 */
+    __shared__ float4 xsh[split ? 1 : 64 * 16]; /* shared mode: 64 items x 16 float4 */
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
     int j = 0;
@@ -2805,17 +2807,28 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     const int s = it >> 2, g = it & 3;
     const size_t row_bytes = (size_t)p.sb * 144;
 
-    /* Shared mode: this thread's part of the activation vector (K / 4 <=
-     * 1024 float4, XS per thread). */
+    /* Shared mode: the activation vector goes straight from memory into LDS
+     * (global_load_lds, no VGPRs). Item i's 16 float4 occupy slots 16i..16i+15
+     * with float4 c in slot 16i + (c ^ (i & 15)): load j of the workgroup
+     * fills items 4j..4j+3 (wave w issues loads j = XW * k + w), each group
+     * of 16 lanes reading one item's 256 contiguous bytes in a permuted order,
+     * and each lane's 16 reads below hit 16 different slots of every 16
+     * consecutive items, so no two lanes of a 16-lane group share a bank.
+     * Lanes past the row's items copy its last item into slots nobody reads. */
     constexpr int XS = 16 / XW;
-    float4 xstage[XS];
-    const int nx4 = 64 * p.sb;
     if constexpr (!split) {
-        /* Threads past the vector repeat its last float4 (no branch, so the
-         * wait for these loads leaves the weight loads below in flight). */
 #pragma unroll
-        for (int i = 0; i < XS; ++i) xstage[i] = ((const float4 *)p.x)[min(tid + 64 * XW * i, nx4 - 1)];
+        for (int k = 0; k < XS; ++k) {
+            const int jl = XW * k + wave;
+            const int item = 4 * jl + (lane >> 4);
+            const int c = (lane & 15) ^ (item & 15);
+            const float4 *src = (const float4 *)p.x + (size_t)min(item, items - 1) * 16 + c;
+            __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(xsh + 64 * jl), 16, 0, 0);
+        }
     }
+    /* Issue order: activations, then weights; the wait for the activations
+     * then leaves the weight loads in flight. */
+    __builtin_amdgcn_sched_barrier(0);
 
     const int qoff = 144 * s + 16 + 32 * g, hoff = 144 * s;
     uint4 qa[RS], qb[RS], hd[RS];
@@ -2827,6 +2840,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
         qb[r] = ld16(base + qoff + 16);
         hd[r] = ld16(base + hoff);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     float xv[64];
     if constexpr (split) {
@@ -2840,16 +2854,22 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
             xv[4 * c + 3] = v.w;
         }
     } else {
-#pragma unroll
-        for (int i = 0; i < XS; ++i) {
-            const int e = min(tid + 64 * XW * i, nx4 - 1);
-            xsh[(e >> 4) * 17 + (e & 15)] = xstage[i];
-        }
-        __syncthreads();
-        const float4 *mine = xsh + it * 17;
+        /* This wave's activation loads (issued first) have landed once at most
+         * the 3 * RS weight loads issued after them are outstanding; then every
+         * wave's have, after the barrier. */
+        constexpr int VM = 3 * RS;
+        static_assert(VM < 64, "vmcnt field");
+        __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+        /* A plain barrier: LDS is coherent within the workgroup once each
+         * wave's loads into it have landed (a fenced __syncthreads would also
+         * wait for the weight loads). */
+        __builtin_amdgcn_s_barrier();
+        /* Slot 16 it + (c ^ (it & 15)) = (16 it + (it & 15)) ^ c, as a byte
+         * offset: one XOR per read. */
+        const uint32_t off0 = (uint32_t)(16 * it + (it & 15)) * 16u;
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            const float4 v = mine[c];
+            const float4 v = *(const float4 *)((const char *)xsh + (off0 ^ (16u * c)));
             xv[4 * c] = v.x;
             xv[4 * c + 1] = v.y;
             xv[4 * c + 2] = v.z;
