@@ -183,22 +183,27 @@ def cpu_variants(qmv, host_layer, batch, seconds):
 
 
 # Single-position Q4_K launches of at most this many (64-row tile, 256-weight
-# unit) pairs run on the row-major kernel (the library's policy, including its
-# QMV_ROWDOT / QMV_ROWDOT_ROWS switches read at start-up).
+# unit) pairs run on the row-major kernel at QMV_ROWDOT_ROWS rows per row
+# segment, larger ones over rows of at most 16 super-blocks at 4 (the
+# library's policy, including its QMV_ROWDOT / QMV_ROWDOT_ROWS switches read
+# at start-up).
 ROWDOT_MAX_UNITS = 2048
+ROWDOT_SHARED_SB = 16
 
 
-def kernel_name(fmt, M, tiled_units=None):
+def kernel_name(fmt, M, tiled_units=None, cols=None):
     """The kernel a Q4_K / Q6_K launch of M positions over `tiled_units`
-    (tile, unit) pairs runs (default tuning)."""
+    (tile, unit) pairs of rows of `cols` columns runs (default tuning)."""
     if M > 8:
         return "prefill_kernel<%s,%d>" % (fmt, 1 if M <= 16 else 2)
     if M >= (7 if fmt == "Q4_K" else 8):
         return "matvec_mfma_kernel<%s,%d>" % (fmt, M)
-    if (fmt == "Q4_K" and M == 1 and tiled_units is not None and tiled_units <= ROWDOT_MAX_UNITS
-            and os.environ.get("QMV_ROWDOT", "1") != "0"):
-        rows = os.environ.get("QMV_ROWDOT_ROWS", "2")
-        return "rowgroup_q4k_kernel<%s,64,0,false>" % (rows if rows in ("1", "2", "4") else "2")
+    if fmt == "Q4_K" and M == 1 and tiled_units is not None and os.environ.get("QMV_ROWDOT", "1") != "0":
+        if tiled_units <= ROWDOT_MAX_UNITS:
+            rows = os.environ.get("QMV_ROWDOT_ROWS", "2")
+            return "rowgroup_q4k_kernel<%s,64,0,false>" % (rows if rows in ("1", "2", "4") else "2")
+        if cols is not None and cols // 256 <= ROWDOT_SHARED_SB:
+            return "rowgroup_q4k_kernel<4,64,0,false>"
     return "matvec_kernel<%s,%d>" % (fmt, M)
 
 
@@ -226,7 +231,7 @@ def build_launches(lib, layers, acts, outs, M):
             return w + 4 * M * cols + 4 * M * sum(T[n].rows for n in names)
 
         def kern(fmt, names, cols):
-            return kernel_name(fmt, M, sum(-(-T[n].rows // 64) * (cols // 256) for n in names))
+            return kernel_name(fmt, M, sum(-(-T[n].rows // 64) * (cols // 256) for n in names), cols)
 
         launches.append((kern("Q4_K", ["q", "k", "v"], HIDDEN), algo(["q", "k", "v"], HIDDEN),
                          grp(["q", "k", "v"], A["attn"]), "qkv"))

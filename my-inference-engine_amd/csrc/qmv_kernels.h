@@ -102,8 +102,7 @@ struct RowdotParams {
     const float *x; /* K activations, shared by all jobs */
     int sb;         /* super-blocks per row */
     /* Fused greedy argmax (QMV_ROWDOT_ARGMAX): candidate tiles as
-     * MatvecParams describes (one per wave, or per workgroup when rows span
-     * waves). */
+     * MatvecParams describes, one per workgroup. */
     uint64_t *argmax_cand;
     unsigned *argmax_count;
     int *argmax_result;

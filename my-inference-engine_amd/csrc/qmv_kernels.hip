@@ -854,15 +854,35 @@ __device__ __forceinline__ bool publish_and_count(uint64_t *slot, uint64_t c, un
 /* Workspace: argmax_cand[tiles + groups] (tile candidates, then group
  * candidates), argmax_count[groups + 1] (group counts, then the top count). */
 template <typename P>
+__device__ __forceinline__ void publish_tile_candidate(const P &p, int tile, float v, int i, int bad, int lane);
+
+/* This lane's row as an argmax candidate (value, index, non-finite flag),
+ * reduced over the wave: every lane ends with the wave's candidate. */
+__device__ __forceinline__ void wave_candidate(bool valid, int row, float y, float &v, int &i, int &bad)
+{
+    const bool fin = isfinite(y);
+    v = valid && fin ? y : -INFINITY;
+    i = valid && fin ? row : 0x7fffffff;
+    bad = valid && !fin;
+    wave_argmax(v, i, bad);
+}
+
+template <typename P>
 __device__ __forceinline__ void tile_argmax(const P &p, int tile, bool valid, int row, float y, int lane)
+{
+    float v;
+    int i, bad;
+    wave_candidate(valid, row, y, v, i, bad);
+    publish_tile_candidate(p, tile, v, i, bad, lane);
+}
+
+/* Publish a tile's candidate (identical in every lane of the calling wave)
+ * and run the group and top levels if this wave arrives last. */
+template <typename P>
+__device__ __forceinline__ void publish_tile_candidate(const P &p, int tile, float v, int i, int bad, int lane)
 {
     const int tiles = p.argmax_tiles;
     const int groups = (tiles + QMV_ARGMAX_GROUP - 1) / QMV_ARGMAX_GROUP;
-    const bool fin = isfinite(y);
-    float v = valid && fin ? y : -INFINITY;
-    int i = valid && fin ? row : 0x7fffffff;
-    int bad = valid && !fin;
-    wave_argmax(v, i, bad);
     const int g = tile / QMV_ARGMAX_GROUP;
     const int first = g * QMV_ARGMAX_GROUP;
     const int in_group = min(QMV_ARGMAX_GROUP, tiles - first);
@@ -2773,11 +2793,10 @@ __device__ __forceinline__ void segment_totals(float v, float (&out)[64 / SEG])
  * (jobs 0 = gate and 1 = up over the same rows: row slots R..2R-1 are job 1's
  * rows, and job 0's y gets up * silu(gate), so the fused result is that of
  * the plain launches' sums bit for bit), QMV_ROWDOT_ARGMAX (one job; y
- * stored, then the greedy argmax of y with one candidate tile per wave in
- * shared mode, per workgroup in split mode). Lane i < R * P of a wave emits
- * the wave's row i. Row sums run in a fixed order (DPP within 16 lanes, the
- * 16-lane rows by readlane, waves through LDS in wave order), so repeated
- * launches are bit-identical. */
+ * stored, then the greedy argmax of y with one candidate tile per
+ * workgroup). Lane i < R * P of a wave emits the wave's row i. Row sums run
+ * in a fixed order (DPP within 16 lanes, the 16-lane rows by readlane, waves
+ * through LDS in wave order), so repeated launches are bit-identical. */
 typedef void __attribute__((address_space(3))) lds_void;
 
 template <int R, int SEG, int EPI, bool SPLIT>
@@ -2958,8 +2977,31 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
             if (job.add != nullptr) out += job.add[row];
             job.y[row] = out;
         }
-        if constexpr (EPI == QMV_ROWDOT_ARGMAX)
-            tile_argmax(p, split ? (int)blockIdx.x : (int)blockIdx.x * XW + wave, valid, row, out, lane);
+        if constexpr (EPI == QMV_ROWDOT_ARGMAX) {
+            if constexpr (split) {
+                tile_argmax(p, (int)blockIdx.x, valid, row, out, lane);
+            } else {
+                /* One candidate per workgroup: the waves' candidates meet in
+                 * LDS and wave 0 publishes their merge. */
+                __shared__ uint64_t wcand[XW];
+                float v;
+                int i, bad;
+                wave_candidate(valid, row, out, v, i, bad);
+                if (lane == 0) wcand[wave] = pack_candidate(v, i, bad);
+                __syncthreads();
+                if (wave != 0) return;
+                float bv = -INFINITY;
+                int bi = 0x7fffffff, bb = 0;
+#pragma unroll
+                for (int w = 0; w < XW; ++w) {
+                    const uint64_t c = wcand[w];
+                    const uint32_t hi = (uint32_t)(c >> 32);
+                    bb |= (int)(hi >> 31);
+                    argmax_merge(bv, bi, __uint_as_float((uint32_t)c), (int)(hi & 0x7fffffffu));
+                }
+                publish_tile_candidate(p, (int)blockIdx.x, bv, bi, bb, lane);
+            }
+        }
     }
 }
 

@@ -491,28 +491,34 @@ int env_int(const char *name, int dflt)
     return atoi(v);
 }
 
-/* Row-major single-position kernel for small Q4_K launches
- * (rowgroup_q4k_kernel). QMV_ROWDOT = 0 turns it off at start-up and
- * qmv_set_rowmajor at run time (tensors uploaded while it is off keep no
- * GGUF copy); QMV_ROWDOT_ROWS / qmv_set_rowmajor set the rows a 64-lane row
- * segment takes (1, 2 or 4; shorter rows' segments take 2). Measured on
- * MI355X in a graph of the Qwen2.5-7B decode set, us per launch, q|k|v / o:
- * tiled 6.81 / 5.80; workgroups of 4 waves sharing the activations in LDS,
- * 1, 2 or 4 rows per wave: 4.85 / 4.19, 4.87 / 4.08, 5.67 / 4.51 (2 rows
- * and per-wave activation loads: 7.1 / 5.8; 2 rows with 1, 2 or 8 waves per
- * workgroup: 5.6 / 4.7, 5.2 / 4.8, 5.8 / 4.0). The tiled plan would split K
- * across workgroups to fill the chip with these launches; gate|up (8288
- * pairs) has enough tiles and stays tiled. */
+/* Row-major single-position kernel for Q4_K launches (rowgroup_q4k_kernel).
+ * QMV_ROWDOT = 0 turns it off at start-up and qmv_set_rowmajor at run time
+ * (tensors uploaded while it is off keep no GGUF copy); QMV_ROWDOT_ROWS /
+ * qmv_set_rowmajor set the rows a 64-lane row segment takes in launches of
+ * at most kRowdotMaxUnits (tile, unit) pairs (1, 2 or 4; shorter rows'
+ * segments take 2). Measured on MI355X in a graph of the Qwen2.5-7B decode
+ * set, us per launch, q|k|v / o: tiled 6.81 / 5.80; workgroups of 4 waves
+ * sharing the activations in LDS, 1, 2 or 4 rows per wave: 4.85 / 4.19,
+ * 4.87 / 4.08, 5.67 / 4.51 (2 rows and per-wave activation loads: 7.1 / 5.8;
+ * 2 rows with 1, 2 or 8 waves per workgroup: 5.6 / 4.7, 5.2 / 4.8,
+ * 5.8 / 4.0). Larger launches of rows of at most 16 super-blocks (gate|up,
+ * 2 x 18944 x 3584: 8288 pairs) take kRowdotRowsLarge = 4 rows per segment:
+ * 16.5 us against 18.1 tiled (2 rows: 19.0, 8 rows: 17.7), and the decode
+ * set 1.139 ms against 1.189 (8 rows: 1.189); longer rows stay tiled there. */
 std::atomic<int> g_rowdot{env_int("QMV_ROWDOT", 1)};
 std::atomic<int> g_rowdot_rows{env_int("QMV_ROWDOT_ROWS", 2)};
 
 /* Super-blocks per row the row-major kernel takes: 8 waves x 64 lanes, 4
  * lanes per super-block. */
 constexpr int kRowdotMaxSb = QMV_MAX_WAVES * 64 / 4;
-/* Launches of at most this many tiled (64-row tile, K-unit) pairs, summed over
- * the launch's tensors, run row-major: Qwen2.5-7B q|k|v (1008) and o (784),
- * not gate|up (8288). */
+/* Launches of up to this many tiled (64-row tile, K-unit) pairs, summed over
+ * the launch's tensors, run row-major with any row length up to
+ * kRowdotMaxSb (Qwen2.5-7B q|k|v: 1008, o: 784); larger ones only with rows
+ * of at most kRowdotSharedSb super-blocks (one LDS copy of the activations
+ * per workgroup), at kRowdotRowsLarge rows per segment. */
 constexpr long long kRowdotMaxUnits = 2048;
+constexpr int kRowdotSharedSb = 16;
+constexpr int kRowdotRowsLarge = 4;
 
 long long tiled_units(int rows, int blocks_per_row)
 {
@@ -523,7 +529,7 @@ long long tiled_units(int rows, int blocks_per_row)
 bool keeps_rowmajor(const QmvGeometry &geo, int rows, int blocks_per_row)
 {
     return g_rowdot.load() != 0 && geo.format == QMV_FMT_Q4_K && blocks_per_row <= kRowdotMaxSb &&
-           tiled_units(rows, blocks_per_row) <= kRowdotMaxUnits;
+           (tiled_units(rows, blocks_per_row) <= kRowdotMaxUnits || blocks_per_row <= kRowdotSharedSb);
 }
 
 /* ---- upload ------------------------------------------------------------------- */
@@ -823,8 +829,9 @@ struct ChunkPlan {
 };
 
 /* A single-position launch of Q4_K tensors on the row-major kernel: every
- * tensor keeps its GGUF bytes, rows fit 8 waves of 16 super-blocks, and the
- * epilogue is at most an added vector. */
+ * tensor keeps its GGUF bytes, rows fit 8 waves of 16 super-blocks (one
+ * wave's segment in launches of more than kRowdotMaxUnits pairs), and the
+ * epilogue is at most an added vector, SwiGLU or the fused argmax. */
 bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
                  const Epilogue &epi, ChunkPlan *cp)
 {
@@ -837,7 +844,12 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         if (ts[i]->rowmajor == nullptr || ts[i]->cols != t0->cols) return false;
         units += tiled_units(ts[i]->rows, ts[i]->blocks_per_row);
     }
-    if (units > kRowdotMaxUnits) return false;
+    /* Large launches: rows of at most kRowdotSharedSb super-blocks, and no
+     * fused argmax (a candidate per 16-row workgroup publishes four times as
+     * often as the tiled kernel's 64-row tiles: 151936 x 3584 Q4_K took 98 us
+     * with the argmax against 69 tiled, 56 against 59 without it). */
+    const bool large = units > kRowdotMaxUnits;
+    if (large && (t0->blocks_per_row > kRowdotSharedSb || epi.argmax)) return false;
     if (epi.swiglu && (count != 2 || ts[1]->rows != t0->rows)) return false; /* rejected by the tiled plan */
     if (epi.argmax && (count != 1 || b0 != 0)) return false;
     const int sb = t0->blocks_per_row;
@@ -848,7 +860,7 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const int seg = sb <= 4 ? 16 : sb <= 8 ? 32 : 64;
     const bool split = sb > 16;
     const int waves = split ? (4 * sb + 63) / 64 : QMV_ROWGROUP_WAVES;
-    const int want = g_rowdot_rows.load();
+    const int want = large ? kRowdotRowsLarge : g_rowdot_rows.load();
     const int R = seg < 64 ? 2 : want == 1 || want == 4 ? want : 2;
     const int wg_rows = split ? R : QMV_ROWGROUP_WAVES * R * (64 / seg);
     qmv::RowdotParams &rp = cp->rp;
@@ -866,9 +878,8 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
         if (epi.add && epi.add[i]) j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
         if (!epi.swiglu || i == 0) wg += (ts[i]->rows + wg_rows - 1) / wg_rows; /* SwiGLU: both jobs in each workgroup */
     }
-    /* Fused argmax candidates: one per wave when a wave's rows are its own,
-     * else one per workgroup. */
-    const long long cand = split ? wg : wg * QMV_ROWGROUP_WAVES;
+    /* Fused argmax candidates: one per workgroup. */
+    const long long cand = wg;
     if (cand > INT_MAX) return false;
     memset(&cp->p, 0, sizeof cp->p);
     cp->rowdot = true;

@@ -69,14 +69,20 @@ def _tiled_units(rows, cols):
     return -(-rows // 64) * (cols // 256)
 
 
+def _keeps_copy(rows, cols):
+    """Launches of up to 2048 tiled pairs, rows of up to 128 super-blocks; any
+    size with rows of up to 16 super-blocks."""
+    sb = cols // 256
+    return sb <= 128 and (_tiled_units(rows, cols) <= SMALL_UNITS or sb <= 16)
+
+
 def _device(qmv, rows, cols, seed):
     raw = qmv.synth_tensor(B.Q4_K, rows, cols, seed=seed)
     dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, rows, cols))
     tiled = -(-rows // 64) * (cols // 256) * 64 * 144
     packed = rows * (cols // 256) * 144
-    small = _tiled_units(rows, cols) <= SMALL_UNITS and cols // 256 <= 128
     # the extra GGUF copy is what routes the tensor's single-position launches
-    assert dt.device_bytes == tiled + (packed if small else 0), (rows, cols, dt.device_bytes)
+    assert dt.device_bytes == tiled + (packed if _keeps_copy(rows, cols) else 0), (rows, cols, dt.device_bytes)
     return raw, dt
 
 
@@ -273,9 +279,56 @@ def test_rowmajor_switched_off(qmv, oracle, gpu, hip):
     dt.close()
 
 
-def test_large_launch_keeps_tiled_layout_only(qmv, gpu):
-    """Gate-sized tensors (Qwen2.5-7B, 18944 x 3584) stay tiled: no extra copy."""
+def test_large_launch_policy(qmv, gpu):
+    """Large launches run row-major only over rows of at most 16 super-blocks:
+    a gate-sized tensor (Qwen2.5-7B, 18944 x 3584, 4144 tiled pairs) keeps the
+    GGUF copy, a long-row one (3584 x 18944, 74 super-blocks, 4144 pairs)
+    stays tiled only."""
     raw = qmv.synth_tensor(B.Q4_K, 18944, 3584, seed=750)
     dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, 18944, 3584))
-    assert dt.device_bytes == 296 * 14 * 64 * 144
+    assert dt.device_bytes == 296 * 14 * 64 * 144 + 18944 * 14 * 144
     dt.close()
+    raw = qmv.synth_tensor(B.Q4_K, 3584, 18944, seed=751)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q4_K, 3584, 18944))
+    assert dt.device_bytes == 56 * 74 * 64 * 144
+    dt.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(18944, 3584), (30000, 1536), (20000, 4096)])
+def test_large_rowmajor_launches(qmv, oracle, gpu, hip, rows, cols):
+    """Launches over more than 2048 tiled pairs (4 rows per segment): a
+    gate|up-shaped group (Qwen2.5-7B 2 x 18944 x 3584), 32-lane segments
+    (K = 1536, two groups of 30000 rows) and 16 super-blocks per row: each
+    row within the oracle's bar, the group's rows equal to each tensor's own
+    launch bit for bit, the fused SwiGLU equal to up * silu(gate) of those
+    rows, and the fused argmax (which runs tiled at these sizes) equal to the
+    argmax of its own logits, which are within the oracle's bar."""
+    log(f"large row-major launch 2 x {rows}x{cols}")
+    (raw_g, dg), (raw_u, du) = _device(qmv, rows, cols, 780), _device(qmv, rows, cols, 781)
+    x = qmv.synth_normal(cols, seed=782)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        g, u, out, lg = (hip.DeviceBuffer(4 * rows) for _ in range(4))
+        res = hip.DeviceBuffer(8)
+        qmv.device_matvec_group([dg, du], dx.ptr, 1, [g.ptr, u.ptr], s.handle)
+        qmv.device_matvec_swiglu(dg, du, dx.ptr, 1, out.ptr, s.handle)
+        qmv.device_matvec_argmax(dg, dx.ptr, lg.ptr, res.ptr, s.handle)
+        s.synchronize()
+        gate, up = g.to_array(np.float32, (rows,)), u.to_array(np.float32, (rows,))
+        _check(oracle, raw_g, rows, cols, x, gate, "gate")
+        _check(oracle, raw_u, rows, cols, x, up, "up")
+        alone = hip.DeviceBuffer(4 * rows)
+        dg.matvec(dx.ptr, 1, alone.ptr, s.handle)
+        s.synchronize()
+        assert np.array_equal(_bits(alone.to_array(np.float32, (rows,))), _bits(gate))
+        logits = lg.to_array(np.float32, (rows,))
+        _check(oracle, raw_g, rows, cols, x, logits, "fused argmax logits")
+        token, finite = res.to_array(np.int32, (2,))
+        assert finite == 1 and token == int(np.argmax(logits))
+        got = out.to_array(np.float32, (rows,)).astype(np.float64)
+        ok, ref = oracle.swiglu(gate, up)
+        assert ok == 1
+        ref = np.asarray(ref, dtype=np.float64)
+        assert (np.abs(got - ref) <= SWIGLU_ULPS * 2.0 ** -23 * np.abs(ref) + 1e-30).all()
+    dg.close()
+    du.close()
