@@ -519,6 +519,11 @@ constexpr int kRowdotMaxSb = QMV_MAX_WAVES * 64 / 4;
 constexpr long long kRowdotMaxUnits = 2048;
 constexpr int kRowdotSharedSb = 16;
 constexpr int kRowdotRowsLarge = 4;
+/* The fused SwiGLU of such launches (gate and up rows in every segment, so
+ * twice the loads in flight per row) takes 2: 16.7-17.8 us against 18.0-18.4
+ * at 4 and 19.1 at 1. A row's sum does not depend on the rows per segment,
+ * so the fused result stays that of the plain launch's rows bit for bit. */
+constexpr int kRowdotRowsLargeSwiglu = 2;
 
 long long tiled_units(int rows, int blocks_per_row)
 {
@@ -860,7 +865,7 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const int seg = sb <= 4 ? 16 : sb <= 8 ? 32 : 64;
     const bool split = sb > 16;
     const int waves = split ? (4 * sb + 63) / 64 : QMV_ROWGROUP_WAVES;
-    const int want = large ? kRowdotRowsLarge : g_rowdot_rows.load();
+    const int want = large ? (epi.swiglu ? kRowdotRowsLargeSwiglu : kRowdotRowsLarge) : g_rowdot_rows.load();
     const int R = seg < 64 ? 2 : want == 1 || want == 4 ? want : 2;
     const int wg_rows = split ? R : QMV_ROWGROUP_WAVES * R * (64 / seg);
     qmv::RowdotParams &rp = cp->rp;
