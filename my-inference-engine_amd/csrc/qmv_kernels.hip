@@ -906,22 +906,14 @@ __device__ __forceinline__ void publish_tile_candidate(const P &p, int tile, flo
 }
 
 /* Index of the job that owns this workgroup (jobs own consecutive ranges of
- * workgroups from their wg_begin). The row-major kernel compares every job
- * boundary at once, so its kernel-argument loads go out together (q|k|v
- * 4.9 -> 4.65 us, o 4.1 -> 3.9 us against a loop over the jobs passed); the
- * tiled kernels walk the jobs, which measured the same or better for them
- * (a single-tensor launch then reads no job boundary: down 3584 x 18944
- * 14.55 us against 14.93). */
-template <typename P>
-__device__ __forceinline__ int job_of_block_all(const P &p)
-{
-    int j = 0;
-#pragma unroll
-    for (int i = 1; i < QMV_MAX_JOBS; ++i)
-        if (i < p.njobs && (int)blockIdx.x >= p.job[i].wg_begin) j = i;
-    return j;
-}
-
+ * workgroups from their wg_begin), walking the jobs: the prefill kernel's
+ * choice. The single-position and matrix-core kernels read every job's start
+ * in one batch of scalar loads instead (launch_args), and so does the
+ * row-major kernel: each dependent kernel-argument load before the first
+ * weight load is a scalar-cache round trip on every wave's critical path
+ * (measured on the Qwen2.5-7B set: q|k|v 4.72 -> 4.60 us, o 3.95 -> 3.83,
+ * gate|up 16.1-16.9 -> 15.7, the fused SwiGLU 16.8-16.9 -> 15.8-16.1, the
+ * M = 8 set 2.282 -> 2.253 ms; down, a single job, unchanged). */
 template <typename P>
 __device__ __forceinline__ int job_of_block(const P &p)
 {
@@ -936,31 +928,85 @@ struct WgWork {
     int job, tile, split, u_begin, u_end;
 };
 
-__device__ __forceinline__ WgWork locate(const MatvecParams &p, int wave, int items)
+/* Kernel arguments a tiled launch needs before its first weight load, read in
+ * one batch of scalar loads: the launch-wide values, job 0's fields, and the
+ * other jobs' first workgroups (unused job slots start past every workgroup,
+ * set by the launchers). The job is the last one starting at or before this
+ * workgroup; a job other than 0 then reads its own fields from lines this
+ * batch brought into the scalar cache. */
+struct LaunchArgs {
+    const float *x;
+    const uint8_t *w; /* the job's tiled weights */
+    int ldx, cols, units, units_per_wave, parts, pair_waves;
+    int job, splits, units_per_split, wg_begin;
+};
+
+__device__ __forceinline__ LaunchArgs launch_args(const MatvecParams &p)
+{
+    LaunchArgs a;
+    a.x = p.x;
+    a.ldx = p.ldx;
+    a.cols = p.cols;
+    a.units = p.units;
+    a.units_per_wave = p.units_per_wave;
+    a.parts = p.parts;
+    a.pair_waves = p.pair_waves;
+    a.w = p.job[0].w;
+    a.splits = p.job[0].splits;
+    a.units_per_split = p.job[0].units_per_split;
+    int begin[QMV_MAX_JOBS];
+#pragma unroll
+    for (int i = 1; i < QMV_MAX_JOBS; ++i) begin[i] = p.job[i].wg_begin;
+    __builtin_amdgcn_sched_barrier(0); /* the loads above go out together */
+    /* Materialise the launch-wide values and job 0's fields here, so the
+     * compiler neither sinks their loads to their first use nor merges job
+     * 0's with the chosen job's into one load that waits for the choice.
+     * The pointers pass as integers and come back as global-memory pointers,
+     * so their loads stay global (not flat) loads. */
+    uint64_t xi = (uint64_t)a.x, wi = (uint64_t)a.w;
+    asm volatile("" : "+s"(xi), "+s"(wi));
+    a.x = (const float *)(const __attribute__((address_space(1))) float *)xi;
+    a.w = (const uint8_t *)(const __attribute__((address_space(1))) uint8_t *)wi;
+    asm volatile("" : "+s"(a.ldx), "+s"(a.cols), "+s"(a.units), "+s"(a.units_per_wave));
+    asm volatile("" : "+s"(a.parts), "+s"(a.pair_waves), "+s"(a.splits), "+s"(a.units_per_split));
+    const int bid = (int)blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < QMV_MAX_JOBS; ++i) j = bid >= begin[i] ? i : j;
+    a.wg_begin = 0;
+    if (a.pair_waves > 0) j = 0; /* paired SwiGLU: job 0's plan serves both halves */
+    a.job = j;
+    if (j != 0) {
+        a.w = p.job[j].w;
+        a.splits = p.job[j].splits;
+        a.units_per_split = p.job[j].units_per_split;
+        a.wg_begin = p.job[j].wg_begin;
+    }
+    return a;
+}
+
+__device__ __forceinline__ WgWork locate(const LaunchArgs &a, int wave, int items)
 {
     WgWork w;
-    if (p.pair_waves > 0) { /* paired SwiGLU: gate waves, then up waves */
-        const int half = wave >= p.pair_waves ? 1 : 0;
-        const MatvecJob &job = p.job[0];
+    if (a.pair_waves > 0) { /* paired SwiGLU (job 0 = gate, 1 = up, same plan): gate waves, then up waves */
+        const int half = wave >= a.pair_waves ? 1 : 0;
         w.job = half;
-        w.tile = blockIdx.x / job.splits;
-        w.split = blockIdx.x - w.tile * job.splits;
-        const int split_begin = w.split * job.units_per_split;
-        const int split_end = min(split_begin + job.units_per_split, p.units);
-        w.u_begin = split_begin + (wave - half * p.pair_waves) * p.units_per_wave;
-        w.u_end = min(w.u_begin + p.units_per_wave, split_end);
+        w.tile = blockIdx.x / a.splits;
+        w.split = blockIdx.x - w.tile * a.splits;
+        const int split_begin = w.split * a.units_per_split;
+        const int split_end = min(split_begin + a.units_per_split, a.units);
+        w.u_begin = split_begin + (wave - half * a.pair_waves) * a.units_per_wave;
+        w.u_end = min(w.u_begin + a.units_per_wave, split_end);
         return w;
     }
-    const int j = job_of_block(p);
-    const MatvecJob &job = p.job[j];
-    const int local = blockIdx.x - job.wg_begin;
-    w.job = j;
-    w.tile = local / job.splits;
-    w.split = local - w.tile * job.splits;
-    const int split_begin = w.split * job.units_per_split;
-    const int split_end = min(split_begin + job.units_per_split, items);
-    w.u_begin = split_begin + wave * p.units_per_wave;
-    w.u_end = min(w.u_begin + p.units_per_wave, split_end);
+    const int local = (int)blockIdx.x - a.wg_begin;
+    w.job = a.job;
+    w.tile = local / a.splits;
+    w.split = local - w.tile * a.splits;
+    const int split_begin = w.split * a.units_per_split;
+    const int split_end = min(split_begin + a.units_per_split, items);
+    w.u_begin = split_begin + wave * a.units_per_wave;
+    w.u_end = min(w.u_begin + a.units_per_wave, split_end);
     return w;
 }
 
@@ -1129,9 +1175,10 @@ matvec_kernel(MatvecParams p)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     /* Batches may run half units (p.parts = 2, one work item per wave): a
      * tile then has 2 x units items, item i being half i & 1 of unit i / 2. */
-    const int shift = M >= 2 && kOne && p.parts == 2 ? 1 : 0;
-    const WgWork w = locate(p, wave, p.units << shift);
-    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
+    const LaunchArgs a = launch_args(p);
+    const int shift = M >= 2 && kOne && a.parts == 2 ? 1 : 0;
+    const WgWork w = locate(a, wave, a.units << shift);
+    const uint8_t *wtile = (w.job == a.job ? a.w : p.job[w.job].w) + (size_t)w.tile * a.units * SLAB;
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
@@ -1141,21 +1188,21 @@ matvec_kernel(MatvecParams p)
             constexpr int R = RegionCount<FMT>::value;
             const int u = w.u_begin >> shift, span = R >> shift;
             const int rb = (w.u_begin - (u << shift)) * span;
-            Unit a;
-            load_unit(a, wtile + (size_t)u * SLAB, lane);
-            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u, lane, acc, rb, rb + span);
+            Unit q;
+            load_unit(q, wtile + (size_t)u * SLAB, lane);
+            unit_step<FMT, M>(q, a.x, a.ldx, a.cols, u, lane, acc, rb, rb + span);
         }
     } else if (w.u_begin < w.u_end) {
         /* Two units in flight per wave: the next unit's planes are loading
          * while the current one is decoded. */
-        Unit a, b;
-        load_unit(a, wtile + (size_t)w.u_begin * SLAB, lane);
+        Unit qa, qb;
+        load_unit(qa, wtile + (size_t)w.u_begin * SLAB, lane);
         for (int u = w.u_begin; u < w.u_end; u += 2) {
             const bool has_b = u + 1 < w.u_end;
-            if (has_b) load_unit(b, wtile + (size_t)(u + 1) * SLAB, lane);
-            unit_step<FMT, M>(a, p.x, p.ldx, p.cols, u, lane, acc);
-            if (u + 2 < w.u_end) load_unit(a, wtile + (size_t)(u + 2) * SLAB, lane);
-            if (has_b) unit_step<FMT, M>(b, p.x, p.ldx, p.cols, u + 1, lane, acc);
+            if (has_b) load_unit(qb, wtile + (size_t)(u + 1) * SLAB, lane);
+            unit_step<FMT, M>(qa, a.x, a.ldx, a.cols, u, lane, acc);
+            if (u + 2 < w.u_end) load_unit(qa, wtile + (size_t)(u + 2) * SLAB, lane);
+            if (has_b) unit_step<FMT, M>(qb, a.x, a.ldx, a.cols, u + 1, lane, acc);
         }
     }
 
@@ -1791,9 +1838,10 @@ matvec_mfma_kernel(MatvecParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int shift = p.parts == 2 ? 1 : 0;
-    const WgWork w = locate(p, wave, p.units << shift);
-    const uint8_t *wtile = p.job[w.job].w + (size_t)w.tile * p.units * SLAB;
+    const LaunchArgs a = launch_args(p);
+    const int shift = a.parts == 2 ? 1 : 0;
+    const WgWork w = locate(a, wave, a.units << shift);
+    const uint8_t *wtile = (w.job == a.job ? a.w : p.job[w.job].w) + (size_t)w.tile * a.units * SLAB;
 
     f32x4_t acc[4];
 #pragma unroll
@@ -1802,8 +1850,8 @@ matvec_mfma_kernel(MatvecParams p)
     if (w.u_begin < w.u_end) {
         const int u = w.u_begin >> shift;
         constexpr int UW = UnitOf<FMT>::kWeights;
-        unit_part_mfma<FMT, M>(wtile + (size_t)u * SLAB, p.x + (size_t)u * UW, p.ldx, lane,
-                               w.u_begin - (u << shift), 1 << shift, p.cols - u * UW, acc);
+        unit_part_mfma<FMT, M>(wtile + (size_t)u * SLAB, a.x + (size_t)u * UW, a.ldx, lane,
+                               w.u_begin - (u << shift), 1 << shift, a.cols - u * UW, acc);
     }
 
     const int kc = lane >> 4, n = lane & 15;
@@ -2745,6 +2793,27 @@ __device__ __forceinline__ void q4_dword_mix2(uint32_t dw, const float *xlo, con
     h = fmaf(f16hi(ho), xhi[3], h);
 }
 
+/* xv[0] + xv[1] + ... + xv[15], in that order. */
+__device__ __forceinline__ float quarter_sum(const float *xv)
+{
+    float t = xv[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) t += xv[e];
+    return t;
+}
+
+/* Workgroup barrier for data exchanged through LDS only: waits for this
+ * wave's LDS operations, not for its global loads (a fenced __syncthreads
+ * would also wait for the weight loads still in flight). The empty asm keeps
+ * the compiler from moving memory accesses across it. */
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0); vmcnt, expcnt not waited */
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 /* Sum of v over each SEG-lane segment of the wave (SEG = 16, 32 or 64), as a
  * wave-uniform value per segment: DPP inside the 16-lane rows, then the rows
  * of a segment by readlane in a fixed order. Every lane must be active. */
@@ -2811,20 +2880,40 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     __shared__ float4 xsh[split ? 1 : 64 * 16]; /* shared mode: 64 items x 16 float4 */
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
-    int j = 0;
-    if constexpr (EPI == QMV_ROWDOT_STORE) j = job_of_block_all(p);
-    const RowdotJob &job = p.job[j];
-    const int local = (int)blockIdx.x - job.wg_begin;
+    /* The job: the last one whose workgroups start at or before this one
+     * (starts ascend; launch_rowgroup sets those of unused job slots past
+     * every workgroup). Every start is read in one batch of scalar loads with
+     * the other arguments the first loads need; the chosen job's fields then
+     * come from lines that batch brought into the scalar cache. */
+    const int bid = (int)blockIdx.x;
+    const uint8_t *jw = p.job[0].w, *const jw1 = p.job[1].w;
+    int jrows = p.job[0].rows, jbegin = 0, j = 0;
+    const int jrows1 = p.job[1].rows, sb = p.sb;
+    const float *const xp = p.x;
+    if constexpr (EPI == QMV_ROWDOT_STORE) {
+        int begin[QMV_MAX_JOBS];
+#pragma unroll
+        for (int i = 1; i < QMV_MAX_JOBS; ++i) begin[i] = p.job[i].wg_begin;
+        __builtin_amdgcn_sched_barrier(0); /* the loads above go out together */
+#pragma unroll
+        for (int i = 1; i < QMV_MAX_JOBS; ++i) j = bid >= begin[i] ? i : j;
+        jw = p.job[j].w;
+        jrows = p.job[j].rows;
+        jbegin = p.job[j].wg_begin;
+    } else {
+        __builtin_amdgcn_sched_barrier(0); /* the loads above go out together */
+    }
+    const int local = bid - jbegin;
     const int row0 = split ? local * R : (local * XW + wave) * (R * P);
     const int seg = P > 1 ? lane / SEG : 0;
-    const int items = 4 * p.sb;
+    const int items = 4 * sb;
     const int it0 = split ? wave * 64 + lane : (lane & (SEG - 1));
     const bool ok = it0 < items;
     /* Lanes past the row's items repeat its last item (in-bounds loads) and
      * drop their sums before the reduction. */
     const int it = min(it0, items - 1);
     const int s = it >> 2, g = it & 3;
-    const size_t row_bytes = (size_t)p.sb * 144;
+    const size_t row_bytes = (size_t)sb * 144;
 
     /* Shared mode: the activation vector goes straight from memory into LDS
      * (global_load_lds, no VGPRs). Item i's 16 float4 occupy slots 16i..16i+15
@@ -2841,7 +2930,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
             const int jl = XW * k + wave;
             const int item = 4 * jl + (lane >> 4);
             const int c = (lane & 15) ^ (item & 15);
-            const float4 *src = (const float4 *)p.x + (size_t)min(item, items - 1) * 16 + c;
+            const float4 *src = (const float4 *)xp + (size_t)min(item, items - 1) * 16 + c;
             __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(xsh + 64 * jl), 16, 0, 0);
         }
     }
@@ -2853,8 +2942,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     uint4 qa[RS], qb[RS], hd[RS];
 #pragma unroll
     for (int r = 0; r < RS; ++r) {
-        const RowdotJob &jr = r < R ? job : p.job[1];
-        const uint8_t *base = jr.w + (size_t)min(row0 + (r % R) * P + seg, jr.rows - 1) * row_bytes;
+        const uint8_t *base = (r < R ? jw : jw1) + (size_t)min(row0 + (r % R) * P + seg, (r < R ? jrows : jrows1) - 1) * row_bytes;
         qa[r] = ld16(base + qoff);
         qb[r] = ld16(base + qoff + 16);
         hd[r] = ld16(base + hoff);
@@ -2863,7 +2951,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
 
     float xv[64];
     if constexpr (split) {
-        const float *xs = p.x + 256 * s + 64 * g;
+        const float *xs = xp + 256 * s + 64 * g;
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
             const float4 v = *(const float4 *)(xs + 4 * c);
@@ -2898,13 +2986,24 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     /* Every load is issued before any arithmetic waits for one. */
     __builtin_amdgcn_sched_barrier(0);
 
+    /* Quarter sums of the item's activations, xq[c] over xv[16c..16c+15] in
+     * order. Shared mode: wave c of the workgroup (whose lanes hold the same
+     * items) sums quarter c alone and the waves exchange them through LDS. */
     float xq[4];
+    if constexpr (split) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        float t = xv[16 * c];
+        for (int c = 0; c < 4; ++c) xq[c] = quarter_sum(xv + 16 * c);
+    } else {
+        static_assert(XW == 4, "one activation quarter per wave");
+        __shared__ float xqs[XW][64];
+        const float t = wave == 0   ? quarter_sum(xv)
+                        : wave == 1 ? quarter_sum(xv + 16)
+                        : wave == 2 ? quarter_sum(xv + 32)
+                                    : quarter_sum(xv + 48);
+        xqs[wave][lane] = t;
+        lds_barrier();
 #pragma unroll
-        for (int e = 1; e < 16; ++e) t += xv[16 * c + e];
-        xq[c] = t;
+        for (int c = 0; c < 4; ++c) xq[c] = xqs[c][lane];
     }
     const float xl = xq[0] + xq[1], xh = xq[2] + xq[3];
     /* Scale/min bytes of sub-blocks 2g, 2g + 1 (header dwords y = bytes
@@ -2919,20 +3018,18 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
 #pragma unroll
     for (int r = 0; r < RS; ++r) {
         /* low / high code sums scaled by 2^-24 (q4_dword_mix2) */
-        float l0 = 0.0f, l1 = 0.0f, h0 = 0.0f, h1 = 0.0f;
+        float l = 0.0f, hs = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            q4_dword_mix2(word(qa[r], e), xv + 4 * e, xv + 32 + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
+        for (int e = 0; e < 4; ++e) q4_dword_mix2(word(qa[r], e), xv + 4 * e, xv + 32 + 4 * e, l, hs);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            q4_dword_mix2(word(qb[r], e), xv + 16 + 4 * e, xv + 48 + 4 * e, (e & 1) ? l1 : l0, (e & 1) ? h1 : h0);
+        for (int e = 0; e < 4; ++e) q4_dword_mix2(word(qb[r], e), xv + 16 + 4 * e, xv + 48 + 4 * e, l, hs);
         const uint4 h = hd[r];
         const uint32_t sc = (((h.w >> sh) & nib) | ((h.y >> shyz) & ~nib)) & 0x3f3fu;
         const uint32_t mn = (((h.w >> (sh + 4)) & nib) | ((h.z >> shyz) & ~nib)) & 0x3f3fu;
         const float d24 = f16_bits_to_f32(h.x) * 16777216.0f, dmin = f16_bits_to_f32(h.x >> 16);
         /* d * 2^24 * (sc_a * L + sc_b * H / 16) - dmin * (m_a * xl + m_b * xh) */
-        float u = ubyte(sc, 0) * (l0 + l1);
-        u = fmaf(ubyte(sc, 1), (h0 + h1) * 0.0625f, u);
+        float u = ubyte(sc, 0) * l;
+        u = fmaf(ubyte(sc, 1), hs * 0.0625f, u);
         float v = ubyte(mn, 0) * xl;
         v = fmaf(ubyte(mn, 1), xh, v);
         float c = d24 * u;
@@ -2965,7 +3062,8 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
                 if constexpr (EPI == QMV_ROWDOT_SWIGLU) up = tot[R + r][q];
             }
     const int row = row0 + lane;
-    const bool valid = lane < R * P && row < job.rows;
+    const RowdotJob &job = p.job[j];
+    const bool valid = lane < R * P && row < jrows;
     if constexpr (EPI == QMV_ROWDOT_SWIGLU) {
         if (valid) {
             if (job.add != nullptr) out += job.add[row];
@@ -3007,6 +3105,15 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
 
 /* ---- host-side launchers -------------------------------------------------- */
 
+/* The tiled kernels pick a workgroup's job among all QMV_MAX_JOBS slots
+ * (launch_args): unused slots start past every workgroup. */
+static MatvecParams with_unused_jobs_last(const MatvecParams &p)
+{
+    MatvecParams q = p;
+    for (int i = q.njobs < 1 ? 1 : q.njobs; i < QMV_MAX_JOBS; ++i) q.job[i].wg_begin = INT_MAX;
+    return q;
+}
+
 template <int FMT, int M>
 static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, hipStream_t s)
 {
@@ -3038,8 +3145,10 @@ static hipError_t launch_matvec_fm(const MatvecParams &p, int grid, int waves, h
 
 #define QMV_LAUNCH(FMT, M) launch_matvec_fm<FMT, M>(p, grid, waves, s)
 
-hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int waves, hipStream_t s)
+hipError_t launch_matvec(int fmt, const MatvecParams &params, int m, int grid, int waves, hipStream_t s)
 {
+    if (params.njobs < 1 || params.njobs > QMV_MAX_JOBS) return hipErrorInvalidValue;
+    const MatvecParams p = with_unused_jobs_last(params);
     switch (fmt) {
     case QMV_FMT_Q4_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q4_K) break;
     case QMV_FMT_Q6_K: QMV_FOR_M(QMV_LAUNCH, QMV_FMT_Q6_K) break;
@@ -3055,10 +3164,15 @@ hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, in
     if (waves < 1 || waves > QMV_MAX_WAVES || grid < 1 || (p.sb <= 16 && waves != QMV_ROWGROUP_WAVES) ||
         (p.sb > 16 && seg != 64))
         return hipErrorInvalidValue;
+    if (p.njobs < 1 || p.njobs > QMV_MAX_JOBS) return hipErrorInvalidValue;
     const bool split = p.sb > 16;
+    /* The kernel picks a workgroup's job among all QMV_MAX_JOBS slots: unused
+     * slots start past every workgroup. */
+    RowdotParams q = p;
+    for (int i = q.njobs; i < QMV_MAX_JOBS; ++i) q.job[i].wg_begin = INT_MAX;
 #define QMV_ROWGROUP(R, SEG, E, SP)                                                                    \
     if (rows == R && seg == SEG && epi == E && split == SP) {                                          \
-        hipLaunchKernelGGL((rowgroup_q4k_kernel<R, SEG, E, SP>), dim3(grid), dim3(waves * 64), 0, s, p); \
+        hipLaunchKernelGGL((rowgroup_q4k_kernel<R, SEG, E, SP>), dim3(grid), dim3(waves * 64), 0, s, q); \
         return hipGetLastError();                                                                      \
     }
 #define QMV_ROWGROUP_E(R, SEG, SP) QMV_ROWGROUP(R, SEG, QMV_ROWDOT_STORE, SP)                         \
