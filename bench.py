@@ -429,7 +429,8 @@ def decode_ops_bench(qmv, hip, stream, layers, reps):
     residual; RoPE and attention are not on this path, so o reads the query
     rows). 6 launches per layer, captured once and replayed between two HIP
     events; then each kind of launch alone (its 28 or 56 launches of a step
-    in one graph) for the time per launch."""
+    in one graph) for the time per launch; then the same step with the norms
+    fused into the projections after them (4 launches per layer)."""
     D = hip.DeviceBuffer
     rng = np.random.default_rng(90)
     vec = lambda n, s: D.from_array((s * rng.standard_normal(n)).astype(np.float32))
@@ -460,6 +461,33 @@ def decode_ops_bench(qmv, hip, stream, layers, reps):
         fns = [fn for k, fn in ops if k == kind]
         per[kind] = round(graph_us(hip, stream, fns, reps) / len(fns), 2)
     out["us_per_launch"] = per
+    # The same step through the fused norm entry points
+    # (qmv_device_rms_norm_matvec_add_group_f32 / _swiglu_f32): 4 calls per
+    # layer; the library fuses the attention norm into the q/k/v launch and
+    # keeps the FFN norm as a launch of its own before the large gate/up
+    # launch, so 5 launches per layer.
+    fused = []
+    for T in layers:
+        fused += [
+            ("norm_qkv_bias", lambda T=T: qmv.device_rms_norm_matvec_add_group(
+                [T["q"], T["k"], T["v"]], x.ptr, w_attn.ptr, eps, 1, [bq.ptr, bk.ptr, bv.ptr], [0, 0, 0],
+                [q.ptr, k.ptr, v.ptr], h.ptr, sp)),
+            ("o_residual", lambda T=T: qmv.device_matvec_add_group([T["o"]], q.ptr, 1, [x.ptr], [HIDDEN], [x.ptr],
+                                                                   sp)),
+            ("norm_gate_up_swiglu", lambda T=T: qmv.device_rms_norm_matvec_swiglu(
+                T["gate"], T["up"], x.ptr, w_ffn.ptr, eps, 1, act.ptr, h.ptr, sp)),
+            ("down_residual", lambda T=T: qmv.device_matvec_add_group([T["down"]], act.ptr, 1, [x.ptr], [HIDDEN],
+                                                                      [x.ptr], sp)),
+        ]
+    fo = {"ms_per_step": round(graph_us(hip, stream, [fn for _, fn in fused], reps) / 1e3, 4),
+          "calls_per_step": len(fused)}
+    fo["residual_finite"] = bool(np.isfinite(x.to_array(np.float32, (HIDDEN,))).all())
+    per = {}
+    for kind in ("norm_qkv_bias", "norm_gate_up_swiglu"):
+        fns = [fn for k, fn in fused if k == kind]
+        per[kind] = round(graph_us(hip, stream, fns, reps) / len(fns), 2)
+    fo["us_per_launch"] = per
+    out["fused_norms"] = fo
     return out
 
 

@@ -243,6 +243,43 @@ int qmv_device_matvec_swiglu_f32(qmv_device_tensor gate, qmv_device_tensor up,
                                  float *d_outputs, void *stream);
 
 /*
+ * RMSNorm of the input fused with the grouped projection that consumes it:
+ * the attention and FFN norms of the reference's decode step
+ * (tensor_rms_norm_f32, src/tensor.cpp:99-136, called before the q/k/v and
+ * the gate/up projections, src/qwen2_architecture.cpp:1241-1260, 1376-1397)
+ * followed by qmv_device_matvec_add_group_f32 / qmv_device_matvec_swiglu_f32
+ * on the normalised vector. No reference counterpart as one call; it replaces
+ * that pair of calls. For each position b,
+ *   h_b = (x_b / sqrt(mean(x_b^2) + epsilon)) * d_norm_weight
+ * and the outputs are those of the plain entry points on h. With one
+ * position and Q4_K tensors whose rows hold at most 16 super-blocks (a
+ * Qwen2.5 hidden size), the norm runs inside the row-major projection
+ * launch: every workgroup normalises the whole input in LDS, so no h is
+ * written and one launch is saved. Otherwise a norm launch writes h to
+ * d_normed (batch_count x K floats, clear of the input, the weights and the
+ * outputs) and the projection reads it; after the call the contents of
+ * d_normed are unspecified. Results are within the row tolerance of the
+ * reference's norm followed by its matvec either way. Argument rules: those
+ * of qmv_device_rms_norm_f32 (epsilon <= 0 fails) and of the plain entry
+ * point; d_addends may be NULL for plain stores.
+ */
+int qmv_device_rms_norm_matvec_add_group_f32(const qmv_device_tensor *tensors,
+                                             int count, const float *d_input,
+                                             const float *d_norm_weight,
+                                             float epsilon, int batch_count,
+                                             const float *const *d_addends,
+                                             const int *addend_strides,
+                                             float *const *d_outputs,
+                                             float *d_normed, void *stream);
+int qmv_device_rms_norm_matvec_swiglu_f32(qmv_device_tensor gate,
+                                          qmv_device_tensor up,
+                                          const float *d_input,
+                                          const float *d_norm_weight,
+                                          float epsilon, int batch_count,
+                                          float *d_output, float *d_normed,
+                                          void *stream);
+
+/*
  * Vocabulary projection fused with greedy sampling: d_logits[N] = W x for one
  * position, and in the same launch d_result[0] = the greedy token (largest
  * logit, lowest id on ties) or -1, d_result[1] = 1 if every logit was finite,

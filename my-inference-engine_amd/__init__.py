@@ -118,6 +118,12 @@ HIP_SIGNATURES = {
                                                        ctypes.POINTER(_vp), _vp]),
     "qmv_device_matvec_swiglu_f32": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _vp, _vp]),
     "qmv_device_rms_norm_f32": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_float, _vp, _vp]),
+    "qmv_device_rms_norm_matvec_add_group_f32": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, _vp, _vp,
+                                                                ctypes.c_float, ctypes.c_int, ctypes.POINTER(_vp),
+                                                                ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_vp),
+                                                                _vp, _vp]),
+    "qmv_device_rms_norm_matvec_swiglu_f32": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_float, ctypes.c_int, _vp,
+                                                             _vp, _vp]),
 }
 
 SYNTH_SIGNATURES = {
@@ -343,6 +349,30 @@ def device_matvec_swiglu(gate: DeviceTensor, up: DeviceTensor, d_x: int, batch: 
 def device_rms_norm(d_x: int, d_weight: int, length: int, batch: int, epsilon: float, d_out: int,
                     stream: int = 0) -> None:
     if not hip_lib().qmv_device_rms_norm_f32(d_x, d_weight, length, batch, epsilon, d_out, stream):
+        raise QmvError(last_error())
+
+
+def device_rms_norm_matvec_add_group(tensors: Sequence[DeviceTensor], d_x: int, d_norm_w: int, epsilon: float,
+                                     batch: int, d_adds: Optional[Sequence[int]], add_strides: Optional[Sequence[int]],
+                                     d_outs: Sequence[int], d_normed: int, stream: int = 0) -> None:
+    """RMSNorm of x (norm weights d_norm_w) fused with the grouped matvec (and
+    its addends, as device_matvec_add_group; None for plain stores). d_normed:
+    batch x K floats the library may use for the normalised input."""
+    n = len(tensors)
+    hs = (ctypes.c_void_p * n)(*[t.handle for t in tensors])
+    adds = (ctypes.c_void_p * n)(*[a or None for a in d_adds]) if d_adds is not None else None
+    lds = (ctypes.c_int * n)(*add_strides) if add_strides is not None else None
+    outs = (ctypes.c_void_p * n)(*d_outs)
+    if not hip_lib().qmv_device_rms_norm_matvec_add_group_f32(hs, n, d_x, d_norm_w, epsilon, batch, adds, lds, outs,
+                                                              d_normed, stream):
+        raise QmvError(last_error())
+
+
+def device_rms_norm_matvec_swiglu(gate: DeviceTensor, up: DeviceTensor, d_x: int, d_norm_w: int, epsilon: float,
+                                  batch: int, d_out: int, d_normed: int, stream: int = 0) -> None:
+    """RMSNorm of x fused with the gate/up projections and SwiGLU."""
+    if not hip_lib().qmv_device_rms_norm_matvec_swiglu_f32(gate.handle, up.handle, d_x, d_norm_w, epsilon, batch,
+                                                           d_out, d_normed, stream):
         raise QmvError(last_error())
 
 

@@ -107,6 +107,12 @@ struct RowdotParams {
     unsigned *argmax_count;
     int *argmax_result;
     int argmax_tiles;
+    /* Fused RMSNorm of the input (launch_rowgroup with norm set; rows of at
+     * most 16 super-blocks): the jobs read (x / sqrt(mean(x^2) + norm_eps)) *
+     * norm_w, the element rule of tensor_rms_norm_f32 (src/tensor.cpp:99-136),
+     * with mean(x^2) over the K = 256 sb inputs. */
+    const float *norm_w;
+    float norm_eps;
 };
 
 /* Row-major epilogues. */
@@ -124,9 +130,11 @@ hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int wa
  * sharing the activations in LDS, each wave taking `rows` (1, 2 or 4) rows
  * per segment of `seg` lanes (16, 32 or 64), so rows * 64 / seg rows per
  * wave. Longer rows (seg = 64): a row spans the workgroup's `waves` waves,
- * `rows` rows per workgroup. */
+ * `rows` rows per workgroup. norm: the fused RMSNorm of RowdotParams (rows
+ * of at most 16 super-blocks; store and SwiGLU epilogues). */
 #define QMV_ROWGROUP_WAVES 4
-hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s);
+hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s,
+                           bool norm = false);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
 /* status (may be null): cleared to 0 if any id is outside [0, rows). */

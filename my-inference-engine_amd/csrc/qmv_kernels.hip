@@ -2849,9 +2849,9 @@ __device__ __forceinline__ void segment_totals(float v, float (&out)[64 / SEG])
  *    one segment of SEG lanes (the smallest of 16, 32, 64 that holds its
  *    items), so a wave holds P = 64 / SEG segments; each wave takes R rows
  *    per segment (rows row0 + w * R * P + r * P + segment). The activation
- *    vector is staged once per workgroup in LDS, each 64-float item padded
- *    by 16 bytes so that the lanes' 128-bit reads are free of bank
- *    conflicts, and every wave reads its items from there.
+ *    vector is staged once per workgroup in LDS, in an XOR-swizzled layout
+ *    that keeps the lanes' 128-bit reads free of bank conflicts, and every
+ *    wave reads its items from there.
  *  - Split (sb > 16, SEG = 64): a row spans the workgroup's waves, which read
  *    their own activations and add their sums in LDS in wave order.
  * Every weight load is issued before any arithmetic; in shared mode the
@@ -2865,19 +2865,33 @@ __device__ __forceinline__ void segment_totals(float v, float (&out)[64 / SEG])
  * stored, then the greedy argmax of y with one candidate tile per
  * workgroup). Lane i < R * P of a wave emits the wave's row i. Row sums run
  * in a fixed order (DPP within 16 lanes, the 16-lane rows by readlane, waves
- * through LDS in wave order), so repeated launches are bit-identical. */
+ * through LDS in wave order), so repeated launches are bit-identical.
+ *
+ * NORM (shared mode): the input is first normalised as tensor_rms_norm_f32
+ * (src/tensor.cpp:99-136) does, h = (x / denom) * w with denom =
+ * sqrt(sum(x^2) / K + eps). The norm weights are staged beside x; each lane
+ * multiplies its item's activations by them and sums their squares, and the
+ * segment adds the lanes' sums in a fixed order that every wave of the launch
+ * repeats (so all find the same denom); each row's sum is divided by denom
+ * before its epilogue:
+ * sum(W (x * w)) / denom, which differs from the reference's
+ * sum(W ((x / denom) * w)) only in rounding. */
 typedef void __attribute__((address_space(3))) lds_void;
 
-template <int R, int SEG, int EPI, bool SPLIT>
+template <int R, int SEG, int EPI, bool SPLIT, bool NORM = false>
 __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(RowdotParams p)
 {
     static_assert(!SPLIT || SEG == 64, "rows that span waves take whole waves");
+    static_assert(!NORM || (!SPLIT && EPI != QMV_ROWDOT_ARGMAX), "the fused norm runs in shared mode, store or SwiGLU");
     constexpr int P = 64 / SEG;
     constexpr int RS = EPI == QMV_ROWDOT_SWIGLU ? 2 * R : R;
     constexpr int XW = QMV_ROWGROUP_WAVES;
     constexpr bool split = SPLIT;
     __shared__ float red[QMV_MAX_WAVES][RS];
-    __shared__ float4 xsh[split ? 1 : 64 * 16]; /* shared mode: 64 items x 16 float4 */
+    /* Shared mode: 64 items x 16 float4 of activations, then (NORM) the norm
+     * weights in the same layout, 16 KiB further. */
+    __shared__ float4 xsh[split ? 1 : (NORM ? 2 : 1) * 64 * 16];
+    float4 *const wsh = xsh + 64 * 16;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
     /* The job: the last one whose workgroups start at or before this one
@@ -2890,6 +2904,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     int jrows = p.job[0].rows, jbegin = 0, j = 0;
     const int jrows1 = p.job[1].rows, sb = p.sb;
     const float *const xp = p.x;
+    const float *const normw = p.norm_w;
     if constexpr (EPI == QMV_ROWDOT_STORE) {
         int begin[QMV_MAX_JOBS];
 #pragma unroll
@@ -2933,6 +2948,16 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
             const float4 *src = (const float4 *)xp + (size_t)min(item, items - 1) * 16 + c;
             __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(xsh + 64 * jl), 16, 0, 0);
         }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int k = 0; k < XS; ++k) {
+                const int jl = XW * k + wave;
+                const int item = 4 * jl + (lane >> 4);
+                const int c = (lane & 15) ^ (item & 15);
+                const float4 *src = (const float4 *)normw + (size_t)min(item, items - 1) * 16 + c;
+                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(wsh + 64 * jl), 16, 0, 0);
+            }
+        }
     }
     /* Issue order: activations, then weights; the wait for the activations
      * then leaves the weight loads in flight. */
@@ -2950,6 +2975,7 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     __builtin_amdgcn_sched_barrier(0);
 
     float xv[64];
+    float norm_total = 0.0f; /* NORM: the vector's sum of squares */
     if constexpr (split) {
         const float *xs = xp + 256 * s + 64 * g;
 #pragma unroll
@@ -2974,13 +3000,43 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
         /* Slot 16 it + (c ^ (it & 15)) = (16 it + (it & 15)) ^ c, as a byte
          * offset: one XOR per read. */
         const uint32_t off0 = (uint32_t)(16 * it + (it & 15)) * 16u;
+        if constexpr (!NORM) {
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            const float4 v = *(const float4 *)((const char *)xsh + (off0 ^ (16u * c)));
-            xv[4 * c] = v.x;
-            xv[4 * c + 1] = v.y;
-            xv[4 * c + 2] = v.z;
-            xv[4 * c + 3] = v.w;
+            for (int c = 0; c < 16; ++c) {
+                const float4 v = *(const float4 *)((const char *)xsh + (off0 ^ (16u * c)));
+                xv[4 * c] = v.x;
+                xv[4 * c + 1] = v.y;
+                xv[4 * c + 2] = v.z;
+                xv[4 * c + 3] = v.w;
+            }
+        } else {
+            /* This item's sum of squares of x, in order, and its activations
+             * times the norm weights, four float4 of each at a time (the
+             * barriers keep the reads from being hoisted, which would hold
+             * 64 more registers). Every segment holds every item of the row,
+             * so the segment total below is the whole vector's. */
+            float ss = 0.0f;
+#pragma unroll
+            for (int c4 = 0; c4 < 16; c4 += 4) {
+#pragma unroll
+                for (int c = c4; c < c4 + 4; ++c) {
+                    const char *const slot = (const char *)xsh + (off0 ^ (16u * c));
+                    const float4 v = *(const float4 *)slot;
+                    const float4 wv = *(const float4 *)(slot + 64 * 16 * 16);
+                    ss = fmaf(v.x, v.x, ss);
+                    ss = fmaf(v.y, v.y, ss);
+                    ss = fmaf(v.z, v.z, ss);
+                    ss = fmaf(v.w, v.w, ss);
+                    xv[4 * c] = v.x * wv.x;
+                    xv[4 * c + 1] = v.y * wv.y;
+                    xv[4 * c + 2] = v.z * wv.z;
+                    xv[4 * c + 3] = v.w * wv.w;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            float tot_ss[P];
+            segment_totals<SEG>(ok ? ss : 0.0f, tot_ss);
+            norm_total = tot_ss[0];
         }
     }
     /* Every load is issued before any arithmetic waits for one. */
@@ -2994,13 +3050,14 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
 #pragma unroll
         for (int c = 0; c < 4; ++c) xq[c] = quarter_sum(xv + 16 * c);
     } else {
-        static_assert(XW == 4, "one activation quarter per wave");
-        __shared__ float xqs[XW][64];
-        const float t = wave == 0   ? quarter_sum(xv)
-                        : wave == 1 ? quarter_sum(xv + 16)
-                        : wave == 2 ? quarter_sum(xv + 32)
-                                    : quarter_sum(xv + 48);
-        xqs[wave][lane] = t;
+        static_assert(XW % 4 == 0, "whole sets of four quarters");
+        __shared__ float xqs[4][64];
+        const int qw = wave & 3;
+        const float t = qw == 0   ? quarter_sum(xv)
+                        : qw == 1 ? quarter_sum(xv + 16)
+                        : qw == 2 ? quarter_sum(xv + 32)
+                                  : quarter_sum(xv + 48);
+        if (wave < 4) xqs[qw][lane] = t;
         lds_barrier();
 #pragma unroll
         for (int c = 0; c < 4; ++c) xq[c] = xqs[c][lane];
@@ -3051,6 +3108,8 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
             tot[r][0] = t;
         }
     }
+    float denom = 1.0f;
+    if constexpr (NORM) denom = sqrtf(norm_total / (float)(256 * sb) + p.norm_eps);
     /* Lane i = r * P + segment emits row row0 + i. */
     float out = tot[0][0], up = tot[RS > R ? R : 0][0];
 #pragma unroll
@@ -3064,6 +3123,10 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     const int row = row0 + lane;
     const RowdotJob &job = p.job[j];
     const bool valid = lane < R * P && row < jrows;
+    if constexpr (NORM) {
+        out /= denom;
+        up /= denom;
+    }
     if constexpr (EPI == QMV_ROWDOT_SWIGLU) {
         if (valid) {
             if (job.add != nullptr) out += job.add[row];
@@ -3159,7 +3222,8 @@ hipError_t launch_matvec(int fmt, const MatvecParams &params, int m, int grid, i
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s)
+hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s,
+                           bool norm)
 {
     if (waves < 1 || waves > QMV_MAX_WAVES || grid < 1 || (p.sb <= 16 && waves != QMV_ROWGROUP_WAVES) ||
         (p.sb > 16 && seg != 64))
@@ -3170,9 +3234,15 @@ hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, in
      * slots start past every workgroup. */
     RowdotParams q = p;
     for (int i = q.njobs; i < QMV_MAX_JOBS; ++i) q.job[i].wg_begin = INT_MAX;
+    if (norm && (split || epi == QMV_ROWDOT_ARGMAX || p.norm_w == nullptr)) return hipErrorInvalidValue;
 #define QMV_ROWGROUP(R, SEG, E, SP)                                                                    \
-    if (rows == R && seg == SEG && epi == E && split == SP) {                                          \
+    if (rows == R && seg == SEG && epi == E && split == SP && !norm) {                                 \
         hipLaunchKernelGGL((rowgroup_q4k_kernel<R, SEG, E, SP>), dim3(grid), dim3(waves * 64), 0, s, q); \
+        return hipGetLastError();                                                                      \
+    }
+#define QMV_ROWGROUP_N(R, SEG, E)                                                                      \
+    if (rows == R && seg == SEG && epi == E && !split && norm) {                                       \
+        hipLaunchKernelGGL((rowgroup_q4k_kernel<R, SEG, E, false, true>), dim3(grid), dim3(waves * 64), 0, s, q); \
         return hipGetLastError();                                                                      \
     }
 #define QMV_ROWGROUP_E(R, SEG, SP) QMV_ROWGROUP(R, SEG, QMV_ROWDOT_STORE, SP)                         \
@@ -3180,7 +3250,12 @@ hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, in
     QMV_ROWGROUP_E(1, 64, false) QMV_ROWGROUP_E(2, 64, false) QMV_ROWGROUP_E(4, 64, false)
     QMV_ROWGROUP_E(2, 32, false) QMV_ROWGROUP_E(2, 16, false)
     QMV_ROWGROUP_E(1, 64, true) QMV_ROWGROUP_E(2, 64, true) QMV_ROWGROUP_E(4, 64, true)
+#define QMV_ROWGROUP_NE(R, SEG) QMV_ROWGROUP_N(R, SEG, QMV_ROWDOT_STORE) QMV_ROWGROUP_N(R, SEG, QMV_ROWDOT_SWIGLU)
+    QMV_ROWGROUP_NE(1, 64) QMV_ROWGROUP_NE(2, 64) QMV_ROWGROUP_NE(4, 64) QMV_ROWGROUP_NE(2, 32)
+    QMV_ROWGROUP_NE(2, 16)
+#undef QMV_ROWGROUP_NE
 #undef QMV_ROWGROUP_E
+#undef QMV_ROWGROUP_N
 #undef QMV_ROWGROUP
     return hipErrorInvalidValue;
 }

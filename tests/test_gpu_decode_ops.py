@@ -241,6 +241,159 @@ def test_rms_norm_kat(qmv, gpu, hip):
     assert dy.to_array(np.float32, (2,)).tolist() == [1.0, 1.5]
 
 
+# ---- RMSNorm fused into the projection that consumes it ------------------------------
+
+NORM_SLACK = 1e-6  # rows: the norm's own rounding (h = x * w then / denom, vs (x / denom) * w)
+
+
+def _norm_inputs(rng, batch, cols, scale):
+    x = (rng.standard_normal((batch, cols)) * scale).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    return x, w
+
+
+def _normed_rows(oracle, raw, t, rows, cols, x, w):
+    """The reference's norm then matvec per position: rows and their bars."""
+    ys, bars = [], []
+    for b in range(x.shape[0]):
+        ok, h = oracle.rms_norm(x[b], w, EPS)
+        assert ok == 1
+        h = np.asarray(h, np.float32)
+        ys.append(np.asarray(oracle.matvec(raw, t, rows, cols, h), np.float64))
+        bars.append((TOL + NORM_SLACK) * oracle.row_stats(raw, t, rows, cols, h)[1])
+    return np.stack(ys), np.stack(bars)
+
+
+@pytest.mark.parametrize("t,shapes,cols,batch,scale", [
+    (B.Q4_K, [3584, 512, 512], 3584, 1, 1.0),    # Qwen2.5-7B attention norm + q/k/v: fused
+    (B.Q4_K, [3584, 512, 512], 3584, 1, 1e-3),   # epsilon comparable to mean(x^2)
+    (B.Q4_K, [1536, 256, 256], 1536, 1, 3.0),    # 6 super-blocks per row: 32-lane segments
+    (B.Q4_K, [1000, 77], 1024, 1, 1.0),          # 4 super-blocks: 16-lane segments, ragged rows
+    (B.Q4_K, [3584, 512, 512], 3584, 3, 1.0),    # three positions: norm launch, then the group
+    (B.Q4_K, [300], 18 * 256, 1, 1.0),           # rows past 16 super-blocks: norm launch
+    (B.Q6_K, [1000], 3584, 1, 1.0),              # not Q4_K: norm launch
+    (B.Q8_0, [896, 128], 896, 2, 1.0),
+])
+def test_rms_norm_fused_matvec_matches_oracle(qmv, oracle, gpu, hip, t, shapes, cols, batch, scale):
+    """qmv_device_rms_norm_matvec_add_group_f32 against the oracle's RMSNorm
+    followed by its matvec and the bias: within the row bar on the normalised
+    input, plus NORM_SLACK for the norm's own rounding (the fused launch
+    scales x by the norm weights and divides each row by the denominator)."""
+    log(f"fused norm + matvec type {t} rows {shapes} K {cols} M={batch} scale {scale}")
+    rng = np.random.default_rng(cols + batch)
+    pairs = [_tensor(qmv, t, r, cols, 150 + i) for i, r in enumerate(shapes)]
+    x, w = _norm_inputs(rng, batch, cols, scale)
+    biases = [(rng.standard_normal(r) * 0.5).astype(np.float32) for r in shapes]
+    dx, dw = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(w)
+    dbias = [hip.DeviceBuffer.from_array(b) for b in biases]
+    dnormed = hip.DeviceBuffer(4 * batch * cols)
+    outs = [hip.DeviceBuffer(4 * batch * r) for r in shapes]
+    stream = hip.Stream()
+    dts = [p[1] for p in pairs]
+    qmv.device_rms_norm_matvec_add_group(dts, dx.ptr, dw.ptr, EPS, batch, [b.ptr for b in dbias], [0] * len(dts),
+                                         [o.ptr for o in outs], dnormed.ptr, stream.handle)
+    stream.synchronize()
+    for i, ((raw, d), r) in enumerate(zip(pairs, shapes)):
+        got = outs[i].to_array(np.float32, (batch, r)).astype(np.float64)
+        ref, bar = _normed_rows(oracle, raw, t, r, cols, x, w)
+        err = np.abs(got - (ref + biases[i][None, :]))
+        assert (err <= bar).all(), f"tensor {i}: {int((err > bar).sum())} rows over the bar"
+    # Plain stores (no addends): the same rows without the bias, to the bar.
+    qmv.device_rms_norm_matvec_add_group(dts, dx.ptr, dw.ptr, EPS, batch, None, None, [o.ptr for o in outs],
+                                         dnormed.ptr, stream.handle)
+    stream.synchronize()
+    raw0 = pairs[0][0]
+    ref, bar = _normed_rows(oracle, raw0, t, shapes[0], cols, x, w)
+    err = np.abs(outs[0].to_array(np.float32, (batch, shapes[0])).astype(np.float64) - ref)
+    assert (err <= bar).all()
+    for d in dts:
+        d.close()
+
+
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q4_K, 18944, 3584, 1), (B.Q4_K, 8960, 1536, 1),
+                                               (B.Q4_K, 18944, 3584, 2), (B.Q6_K, 1000, 3584, 1)])
+def test_rms_norm_fused_swiglu_matches_oracle(qmv, oracle, gpu, hip, t, rows, cols, batch):
+    """qmv_device_rms_norm_matvec_swiglu_f32 against the oracle's RMSNorm,
+    gate and up matvecs and SwiGLU: each projection within its bar (as above),
+    carried through silu(g) * u (|d silu / dg| <= 1.1), plus SWIGLU_ULPS."""
+    log(f"fused norm + SwiGLU type {t} {rows}x{cols} M={batch}")
+    rng = np.random.default_rng(rows + batch)
+    raw_g, dg = _tensor(qmv, t, rows, cols, 160)
+    raw_u, du = _tensor(qmv, t, rows, cols, 161)
+    x, w = _norm_inputs(rng, batch, cols, 1.0)
+    dx, dw = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(w)
+    dnormed = hip.DeviceBuffer(4 * batch * cols)
+    dout = hip.DeviceBuffer(4 * batch * rows)
+    stream = hip.Stream()
+    qmv.device_rms_norm_matvec_swiglu(dg, du, dx.ptr, dw.ptr, EPS, batch, dout.ptr, dnormed.ptr, stream.handle)
+    stream.synchronize()
+    got = dout.to_array(np.float32, (batch, rows)).astype(np.float64)
+    g_ref, g_bar = _normed_rows(oracle, raw_g, t, rows, cols, x, w)
+    u_ref, u_bar = _normed_rows(oracle, raw_u, t, rows, cols, x, w)
+    with np.errstate(over="ignore"):  # exp(-g) overflows to inf for g < -88 in float32 terms; silu -> -0
+        silu = g_ref / (1.0 + np.exp(-g_ref))
+    ref = u_ref * silu
+    bar = 1.1 * np.abs(u_ref) * g_bar + np.abs(silu) * u_bar + g_bar * u_bar + SWIGLU_ULPS * 2.0 ** -23 * np.abs(ref)
+    err = np.abs(got - ref)
+    assert (err <= bar + 1e-30).all(), f"{int((err > bar).sum())} elements over the bar"
+    dg.close()
+    du.close()
+
+
+def test_rms_norm_fused_graph_replays(qmv, gpu, hip):
+    """The fused launch captured in a graph replays to the eager bits, with
+    eager launches of other work between the replays."""
+    cols = 3584
+    _, dq = _tensor(qmv, B.Q4_K, 3584, cols, 170)
+    _, dk = _tensor(qmv, B.Q4_K, 512, cols, 171)
+    rng = np.random.default_rng(172)
+    x, w = _norm_inputs(rng, 1, cols, 1.0)
+    dx, dw = hip.DeviceBuffer.from_array(x), hip.DeviceBuffer.from_array(w)
+    dnormed = hip.DeviceBuffer(4 * cols)
+    yq, yk, other = hip.DeviceBuffer(4 * 3584), hip.DeviceBuffer(4 * 512), hip.DeviceBuffer(4 * 3584)
+    with hip.Stream() as stream:
+        call = lambda: qmv.device_rms_norm_matvec_add_group([dq, dk], dx.ptr, dw.ptr, EPS, 1, None, None,
+                                                            [yq.ptr, yk.ptr], dnormed.ptr, stream.handle)
+        call()
+        stream.synchronize()
+        eager = (yq.to_array(np.float32, (3584,)).copy(), yk.to_array(np.float32, (512,)).copy())
+        with hip.Graph(stream) as g:
+            g.begin()
+            call()
+            g.end()
+            for i in range(3):
+                yq.fill(0)
+                yk.fill(0)
+                g.replay()
+                stream.synchronize()
+                assert np.array_equal(_bits(yq.to_array(np.float32, (3584,))), _bits(eager[0])), i
+                assert np.array_equal(_bits(yk.to_array(np.float32, (512,))), _bits(eager[1])), i
+                qmv.device_matvec_group([dq], dx.ptr, 1, [other.ptr], stream.handle)
+                stream.synchronize()
+    dq.close()
+    dk.close()
+
+
+def test_rms_norm_fused_argument_rules(qmv, gpu, hip):
+    cols = 1536
+    _, dq = _tensor(qmv, B.Q4_K, 256, cols, 180)
+    dx = hip.DeviceBuffer.from_array(qmv.synth_normal(cols, seed=181))
+    dw = hip.DeviceBuffer.from_array(np.ones(cols, np.float32))
+    y, dn = hip.DeviceBuffer(4 * 256), hip.DeviceBuffer(4 * cols)
+    with pytest.raises(qmv.QmvError, match="RMSNorm arguments"):
+        qmv.device_rms_norm_matvec_add_group([dq], dx.ptr, dw.ptr, 0.0, 1, None, None, [y.ptr], dn.ptr, 0)
+    with pytest.raises(qmv.QmvError, match="RMSNorm arguments"):
+        qmv.device_rms_norm_matvec_add_group([dq], dx.ptr, 0, EPS, 1, None, None, [y.ptr], dn.ptr, 0)
+    with pytest.raises(qmv.QmvError, match="d_normed overlaps"):
+        qmv.device_rms_norm_matvec_add_group([dq], dx.ptr, dw.ptr, EPS, 1, None, None, [y.ptr], dx.ptr, 0)
+    with pytest.raises(qmv.QmvError, match="d_normed overlaps an output"):
+        qmv.device_rms_norm_matvec_add_group([dq], dx.ptr, dw.ptr, EPS, 1, None, None, [y.ptr], y.ptr, 0)
+    with pytest.raises(qmv.QmvError, match="share type, shape"):
+        _, du = _tensor(qmv, B.Q4_K, 128, cols, 182)
+        qmv.device_rms_norm_matvec_swiglu(dq, du, dx.ptr, dw.ptr, EPS, 1, y.ptr, dn.ptr, 0)
+    dq.close()
+
+
 # ---- the decode step's projections chained on device, replayed as a graph ----------
 
 def test_decode_layer_chain_graph(qmv, oracle, gpu, hip):
