@@ -1911,6 +1911,12 @@ template <int KL, int P, int UW = 256> struct PfLayout {
     static constexpr int kPerThread = kChunks / (QMV_PF_WAVES * 64);
     static constexpr int kBytes = 3 * P * kBlocks * kFrag; /* 24 KB per position block */
     __device__ static int offset(int limb, int pb, int b) { return ((limb * P + pb) * kBlocks + b) * kFrag; }
+    /* Q4_K: the sub-block sums of the activations as an A operand of 8
+     * sub-blocks (fragment (limb, pb): lane n < 16 holds limb L of
+     * sum(x[16 pb + n][32 s .. 32 s + 31]) for s = 0..7; lanes 16..63 hold
+     * zeros), after the limb images. */
+    static constexpr int kSxBytes = 3 * P * 64 * 16;
+    __device__ static int sx_offset(int limb, int pb) { return kBytes + (limb * P + pb) * 64 * 16; }
 };
 
 /* Chunk c of a unit: lane = c % 64, block b, position block pb. Blocks from
@@ -1937,7 +1943,7 @@ __device__ __forceinline__ void pf_load_x(const float *xu, int ldx, int npos, in
     }
 }
 
-template <int KL, int P, int UW = 256>
+template <int KL, int P, int UW = 256, bool kSubSums = false>
 __device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid,
                                                const float (&xr)[PfLayout<KL, P, UW>::kPerThread][KL])
 {
@@ -1953,6 +1959,28 @@ __device__ __forceinline__ void pf_store_limbs(lds_u8 *lds, int tid,
         *(lds_frag *)(lds + L::offset(0, pb, b) + lane * 2 * KL) = h;
         *(lds_frag *)(lds + L::offset(1, pb, b) + lane * 2 * KL) = m;
         *(lds_frag *)(lds + L::offset(2, pb, b) + lane * 2 * KL) = l;
+        if constexpr (kSubSums) {
+            /* Sub-block b's sum for position 16 pb + n: this lane's KL
+             * activations in order, then the four lanes n + 16 kc (the
+             * chunk's k quarters) pairwise, the same bits in all four. */
+            static_assert(KL == 8, "Q4_K sub-blocks: four chunks of 8");
+            float t = xr[i][0];
+#pragma unroll
+            for (int j = 1; j < KL; ++j) t += xr[i][j];
+            t += __shfl_xor(t, 16);
+            t += __shfl_xor(t, 32);
+            if (lane < 16) {
+                const __bf16 th = (__bf16)t;
+                const float r = t - (float)th;
+                const __bf16 tm = (__bf16)r;
+                const __bf16 tl = (__bf16)(r - (float)tm);
+                typedef __attribute__((address_space(3))) __bf16 lds_bf16;
+                const int at = lane * 16 + b * 2;
+                *(lds_bf16 *)(lds + L::sx_offset(0, pb) + at) = th;
+                *(lds_bf16 *)(lds + L::sx_offset(1, pb) + at) = tm;
+                *(lds_bf16 *)(lds + L::sx_offset(2, pb) + at) = tl;
+            }
+        }
     }
 }
 
@@ -1973,8 +2001,32 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
     for (int g = 0; g < 4; ++g) q[0][g] = q0[g];
     uint4 hn[4];
     uint2 qn[4];
-    const bf16x8_t ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
-                           (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
+    /* The minimum terms of the whole unit on the matrix cores:
+     * sum_s m_s * sum(x over sub-block s) per row and position, with the
+     * staged sub-block sums (exact limbs) as A, k = s < 8, and each row's 8
+     * six-bit minimums (exact in bf16) as B; then acc -= dmin * that once. */
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const uint4 hg = h[g];
+        const uint32_t mlo = hg.z & 0x3f3f3f3fu;
+        const uint32_t mhi = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
+        const bf16x8_t bm = {(__bf16)ubyte(mlo, 0), (__bf16)ubyte(mlo, 1), (__bf16)ubyte(mlo, 2),
+                             (__bf16)ubyte(mlo, 3), (__bf16)ubyte(mhi, 0), (__bf16)ubyte(mhi, 1),
+                             (__bf16)ubyte(mhi, 2), (__bf16)ubyte(mhi, 3)};
+        const float dmin = f16_bits_to_f32(hg.x >> 16);
+#pragma unroll
+        for (int pb = 0; pb < P; ++pb) {
+            typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
+            f32x4_t dm = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int limb = 0; limb < 3; ++limb)
+                dm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(lds_a *)(lds + L::sx_offset(limb, pb) + lane * 16), bm,
+                                                             dm, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[pb][g][j] = fmaf(-dmin, dm[j], acc[pb][g][j]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         const int c = sb >> 1;
@@ -1996,7 +2048,7 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
 #pragma unroll
         for (int g = 0; g < 4; ++g)
             b[g] = q4_codes_bf16(q[c & 1][g].x, q[c & 1][g].y, high);
-        float sa[4], sm[4];
+        float sa[4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
             typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
@@ -2004,40 +2056,29 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
             const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, sb));
             const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, sb));
             const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, sb));
-            f32x4_t xs = {0.0f, 0.0f, 0.0f, 0.0f}, d[4];
+            f32x4_t d[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, xs, 0, 0, 0);
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
-            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
-            xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, ones, xs, 0, 0, 0);
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
             if (pb == 0) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const uint4 hg = h[g];
-                    const float dd = f16_bits_to_f32(hg.x), dmin = f16_bits_to_f32(hg.x >> 16);
-                    uint32_t scw, mw;
-                    if (sb < 4) {
-                        scw = hg.y & 0x3f3f3f3fu;
-                        mw = hg.z & 0x3f3f3f3fu;
-                    } else {
-                        scw = (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
-                        mw = ((hg.w >> 4) & 0x0f0f0f0fu) | ((hg.z >> 2) & 0x30303030u);
-                    }
+                    const float dd = f16_bits_to_f32(hg.x);
+                    const uint32_t scw =
+                        sb < 4 ? hg.y & 0x3f3f3f3fu : (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
                     sa[g] = dd * ubyte(scw, sb & 3);
-                    sm[g] = dmin * ubyte(mw, sb & 3);
                 }
             }
 #pragma unroll
             for (int g = 0; g < 4; ++g)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[pb][g][j] = fmaf(sa[g], d[g][j], fmaf(-sm[g], xs[j], acc[pb][g][j]));
+                for (int j = 0; j < 4; ++j) acc[pb][g][j] = fmaf(sa[g], d[g][j], acc[pb][g][j]);
         }
         /* One sub-block's codes and scales live at a time. */
         __builtin_amdgcn_sched_barrier(0);
@@ -2408,7 +2449,9 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
     using L = PfLayout<KL, P, UW>;
     /* The combine buffer (each wave's tile, MP x 64 floats) reuses the
      * staging buffer. */
-    constexpr int kLds = L::kBytes > QMV_PF_WAVES * MP * 64 * 4 ? L::kBytes : QMV_PF_WAVES * MP * 64 * 4;
+    constexpr bool kSubSums = FMT == QMV_FMT_Q4_K; /* the minimum terms on the matrix cores (q4k_unit_pf) */
+    constexpr int kStage = L::kBytes + (kSubSums ? L::kSxBytes : 0);
+    constexpr int kLds = kStage > QMV_PF_WAVES * MP * 64 * 4 ? kStage : QMV_PF_WAVES * MP * 64 * 4;
     __shared__ __attribute__((aligned(16))) uint8_t lds_buf[kLds];
     lds_u8 *lds = (lds_u8 *)lds_buf;
 
@@ -2466,10 +2509,17 @@ __global__ void __launch_bounds__(QMV_PF_WAVES * 64) prefill_kernel(MatvecParams
     }
     float xr[L::kPerThread][KL];
     pf_load_x<KL, P, UW>(p.x + (size_t)w.u_begin * UW, p.ldx, npos, tid, xr, p.cols - w.u_begin * UW);
+    if constexpr (kSubSums) {
+        /* Lanes 16..63 of the sub-sum fragments stay zero (only lanes 0..15
+         * are rewritten per unit); the first barrier below orders this. */
+        typedef __attribute__((address_space(3))) u32v4 lds_v4;
+        for (int i = tid; i < L::kSxBytes / 16; i += QMV_PF_WAVES * 64)
+            *(lds_v4 *)(lds + L::kBytes + 16 * i) = u32v4{0u, 0u, 0u, 0u};
+    }
 
     for (int u = w.u_begin; u < w.u_end; ++u) {
         __syncthreads(); /* every wave is done with the previous unit's image */
-        pf_store_limbs<KL, P, UW>(lds, tid, xr);
+        pf_store_limbs<KL, P, UW, kSubSums>(lds, tid, xr);
         __syncthreads();
         if (u + 1 < w.u_end)
             pf_load_x<KL, P, UW>(p.x + (size_t)(u + 1) * UW, p.ldx, npos, tid, xr, p.cols - (u + 1) * UW);
