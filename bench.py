@@ -184,8 +184,9 @@ def cpu_variants(qmv, host_layer, batch, seconds):
 
 # Single-position Q4_K launches of at most this many (64-row tile, 256-weight
 # unit) pairs run on the row-major kernel at QMV_ROWDOT_ROWS rows per row
-# segment, larger ones over rows of at most 16 super-blocks at 4 (the
-# library's policy, including its QMV_ROWDOT / QMV_ROWDOT_ROWS switches read
+# segment, larger ones over rows of at most 16 super-blocks at 4; Q6_K rows
+# of 17 to 128 super-blocks run on the row-loop kernel (the library's policy,
+# including its QMV_ROWDOT / QMV_ROWDOT_ROWS / QMV_ROWDOT_Q6K switches read
 # at start-up).
 ROWDOT_MAX_UNITS = 2048
 ROWDOT_SHARED_SB = 16
@@ -198,7 +199,12 @@ def kernel_name(fmt, M, tiled_units=None, cols=None):
         return "prefill_kernel<%s,%d>" % (fmt, 1 if M <= 16 else 2)
     if M >= (7 if fmt == "Q4_K" else 8):
         return "matvec_mfma_kernel<%s,%d>" % (fmt, M)
-    if fmt == "Q4_K" and M == 1 and tiled_units is not None and os.environ.get("QMV_ROWDOT", "1") != "0":
+    rowdot = os.environ.get("QMV_ROWDOT", "1") != "0"
+    if fmt == "Q6_K" and M == 1 and cols is not None and rowdot and os.environ.get("QMV_ROWDOT_Q6K", "1") != "0":
+        sb = cols // 256
+        if ROWDOT_SHARED_SB < sb <= 128:
+            return "rowloop_q6k_kernel<%d,2>" % (-(-sb // 16))
+    if fmt == "Q4_K" and M == 1 and tiled_units is not None and rowdot:
         if tiled_units <= ROWDOT_MAX_UNITS:
             rows = os.environ.get("QMV_ROWDOT_ROWS", "2")
             return "rowgroup_q4k_kernel<%s,64,0,false>" % (rows if rows in ("1", "2", "4") else "2")

@@ -85,8 +85,9 @@ struct MatvecParams {
     int pair_waves;
 };
 
-/* One tensor of a row-major single-position launch (Q4_K): `w` holds the
- * GGUF bytes of the tensor (row r at r * sb * 144), workgroups
+/* One tensor of a row-major single-position launch: `w` holds the GGUF bytes
+ * of a Q4_K tensor (row r at r * sb * 144) or the planes of a Q6_K tensor
+ * (row r at r * q6k_row_stride(sb), launch_rowmajor_q6k), workgroups
  * [wg_begin, next job's wg_begin) take consecutive rows. */
 struct RowdotJob {
     const uint8_t *w;
@@ -113,6 +114,9 @@ struct RowdotParams {
      * with mean(x^2) over the K = 256 sb inputs. */
     const float *norm_w;
     float norm_eps;
+    /* Q6_K (launch_rowloop_q6k): the launch's rows (its jobs' rows in job
+     * order); each job's wg_begin is its first row there. */
+    int groups;
 };
 
 /* Row-major epilogues. */
@@ -135,6 +139,20 @@ hipError_t launch_matvec(int fmt, const MatvecParams &p, int m, int grid, int wa
 #define QMV_ROWGROUP_WAVES 4
 hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, int grid, int waves, hipStream_t s,
                            bool norm = false);
+/* Row-major Q6_K: bytes per row of the chunked plane layout
+ * launch_rowmajor_q6k writes (210 per super-block, the row padded to 16
+ * bytes). */
+__host__ __device__ inline size_t q6k_row_stride(int sb) { return ((size_t)210 * sb + 15) & ~(size_t)15; }
+/* Row-major Q6_K launch at one position over rows of 17 to 128
+ * super-blocks: `grid` workgroups of `waves` (1 to 16) waves, one row per
+ * wave, over the launch's p.groups rows (grid = ceil(p.groups / waves)).
+ * epi: QMV_ROWDOT_STORE (plus the optional addends), QMV_ROWDOT_SWIGLU (jobs
+ * 0 and 1 of equal rows; p.groups = their rows) or QMV_ROWDOT_ARGMAX (one
+ * job, one candidate per workgroup: p.argmax_tiles = grid). */
+hipError_t launch_rowloop_q6k(const RowdotParams &p, int epi, int grid, int waves, hipStream_t s);
+/* The Q6_K plane layout of `rows` GGUF rows of sb super-blocks (raw, 210
+ * bytes each) into out (rows * q6k_row_stride(sb) bytes; padding untouched). */
+hipError_t launch_rowmajor_q6k(const uint8_t *raw, uint8_t *out, int rows, int sb, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,
                           int first_row, int row_count, hipStream_t s);
 /* status (may be null): cleared to 0 if any id is outside [0, rows). */

@@ -3248,6 +3248,292 @@ __global__ void __launch_bounds__(QMV_MAX_WAVES * 64) rowgroup_q4k_kernel(Rowdot
     }
 }
 
+/* ---- row-major Q6_K at one position ------------------------------------------
+ * A Q6_K row of sb super-blocks is kept as chunks of 16 super-blocks (the
+ * last one m = sb - 16 (ceil(sb / 16) - 1)), chunk c at 3360 c (16 x 210
+ * bytes), each in five planes (rowmajor_q6k_kernel writes them from the GGUF
+ * row; q6k_row_stride(sb) bytes per row, 210 sb rounded up to 16):
+ *   A at 0        64 bytes per super-block: ql[0..31], ql[64..95]
+ *   B at 64 m     ql[32..63], ql[96..127]
+ *   H at 128 m    qh[0..63]
+ *   S at 192 m    16 scale bytes per super-block, reordered (below)
+ *   D at 208 m    the super-block's f16 d
+ * Item i = 4s + q of a chunk (local super-block s, q = 0..3, half n = q / 2,
+ * l0 = 16 (q % 2)) is the 64 weights 128n + l0 + 32k + [0, 16), k = 0..3,
+ * of that super-block: bytes 16i..16i+15 of A (low nibbles k = 0, high
+ * nibbles k = 2), of B (k = 1, 3) and of H (bits 2k..2k+1 for run k), and
+ * the four scales of its sub-blocks 8n + q % 2 + 2k as the bytes k of dword
+ * i of S. A weight's code is low | high << 4, its value (code - 32) * d *
+ * scale, as the GGUF block defines it (ql[l] low nibble: weight l of the
+ * half, ql[l] high: 64 + l, ql[32 + l]: 32 + l and 96 + l, qh[l] bits 0-1,
+ * 2-3, 4-5, 6-7: weights l, 32 + l, 64 + l, 96 + l). A wave reads a chunk's
+ * planes with consecutive lanes at consecutive addresses, 3360 contiguous
+ * bytes per chunk. */
+
+/* Thread per byte of a GGUF super-block: its place in the planes. */
+__global__ void rowmajor_q6k_kernel(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int sb,
+                                    long long total)
+{
+    const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int i = (int)(id % 210);
+    const long long blk = id / 210; /* row * sb + s */
+    const int sg = (int)(blk % sb);
+    const long long row = blk / sb;
+    /* chunk c = sg / 16 of m super-blocks, local super-block s */
+    const int c = sg >> 4, s = sg & 15, m = min(16, sb - 16 * c);
+    size_t off = (size_t)3360 * c;
+    if (i < 128) { /* ql: plane A (w < 32) or B, item 2n + (w / 16) % 2 */
+        const int n = i >> 6, w = i & 63;
+        off += (w >> 5) * 64 * m + 64 * s + 16 * (2 * n + ((w >> 4) & 1)) + (w & 15);
+    } else if (i < 192) { /* qh in order */
+        off += 128 * m + 64 * s + (i - 128);
+    } else if (i < 208) { /* scale of sub-block t = 8n + 2k + odd -> item 2n + odd, byte k */
+        const int t = i - 192, n = t >> 3, odd = t & 1, k = (t & 7) >> 1;
+        off += 192 * m + 16 * s + 4 * (2 * n + odd) + k;
+    } else {
+        off += 208 * m + 2 * s + (i - 208);
+    }
+    out[row * q6k_row_stride(sb) + off] = raw[blk * 210 + i];
+}
+
+/* Row-major Q6_K matvec at one position (rows of more than 16 super-blocks).
+ * Each wave computes whole rows: a row is NSL = ceil(sb / 16) slices of up
+ * to 16 super-blocks (the row's contiguous plane chunks), one 64-weight item
+ * per lane and slice, and the wave takes the slices in turn, loading the next
+ * slice's weights before it computes the current one; the lane's sums over
+ * its slices are added by DPP, so a row's result is the same in any launch.
+ * Workgroup b takes rows b * W .. b * W + W - 1 of the launch (W waves, one
+ * row each; the launch's rows are its jobs' rows in job order). The
+ * workgroup first copies the activations, straight from memory, into LDS
+ * (global_load_lds, 1 KiB contiguous per instruction, 16 KiB per slice),
+ * and the four run sums of every slice item into LDS beside them; a lane
+ * then reads its item's 64 activations (16 ds_read_b128) and run sums for
+ * each slice. EPI: QMV_ROWDOT_STORE (y = sum, plus `add` if set),
+ * QMV_ROWDOT_SWIGLU (a wave takes gate row r of job 0, then up row r of job
+ * 1, and job 0's y gets up * silu(gate): the plain launch's sums bit for
+ * bit), QMV_ROWDOT_ARGMAX (one job; y stored, then the greedy argmax of y
+ * with one candidate per workgroup).
+ *
+ * LDS layout of a slice: 16-byte chunk g of its activations (g = 64 s' +
+ * 32 n + 8 k + 4 h + c for local super-block s', half n, run k, item half
+ * h = q % 2 and float4 c of the run) sits in slot g ^ m(g), m(g) = bit 5 of
+ * g to bit 0, bit 6 to bit 1, bit 7 to bit 3. A read (k, c) of the 16 lanes
+ * of a 16-lane group (4 super-blocks x 4 items) then lands on 16 different
+ * slots mod 16 (bits 0..3 = c0 ^ n, c1 ^ s'0, h, k0 ^ s'1), so no two of
+ * them share a bank. The copy writes slot 64 j + lane of instruction j,
+ * reading chunk slot ^ m(slot) (m only reads bits the XOR leaves alone). */
+__device__ __forceinline__ int q6k_slot_mix(int g)
+{
+    return ((g >> 5) & 1) | (((g >> 6) & 1) << 1) | (((g >> 7) & 1) << 3);
+}
+
+/* One lane's item of one slice of a row: A, B and H plane pieces, scale
+ * dword, d. */
+struct Q6Item {
+    uint4 a, b, h;
+    uint32_t sc, dd;
+};
+
+/* Slice j's item of lane it (< 4 m) in the row at `row`: the chunk holds m
+ * super-blocks. */
+__device__ __forceinline__ Q6Item q6k_load_item(gu8 *row, int j, int m, int it)
+{
+    gu8 *base = row + 3360 * j;
+    Q6Item w;
+    w.a = gload16(base + 16 * it);
+    w.b = gload16(base + 64 * m + 16 * it);
+    w.h = gload16(base + 128 * m + 16 * it);
+    w.sc = *(gu32 *)(base + 192 * m + 4 * it);
+    w.dd = *(gu16 *)(base + 208 * m + 2 * (it >> 2));
+    return w;
+}
+
+/* The item's lane sum: d * sum_k scale_k * (sum(code x) - 32 sum(x)) over
+ * its four runs (xq: their sums). */
+__device__ __forceinline__ float q6k_item_sum(const Q6Item &w, const float *xv, float4 xq)
+{
+    /* run sums of code * x, scaled by 2^-24 (byte_codes_mix) */
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t aw = word(w.a, e), bw = word(w.b, e), hw = word(w.h, e);
+        const uint32_t q0 = codes((aw & 0x0f0f0f0fu) | ((hw << 4) & 0x30303030u));
+        const uint32_t q1 = codes((bw & 0x0f0f0f0fu) | ((hw << 2) & 0x30303030u));
+        const uint32_t q2 = codes(((aw >> 4) & 0x0f0f0f0fu) | (hw & 0x30303030u));
+        const uint32_t q3 = codes(((bw >> 4) & 0x0f0f0f0fu) | ((hw >> 2) & 0x30303030u));
+        s0 = byte_codes_mix(q0, xv + 4 * e, s0);
+        s1 = byte_codes_mix(q1, xv + 16 + 4 * e, s1);
+        s2 = byte_codes_mix(q2, xv + 32 + 4 * e, s2);
+        s3 = byte_codes_mix(q3, xv + 48 + 4 * e, s3);
+    }
+    /* the offset term scaled by 2^-24 like the sums (32 * 2^-24 = 2^-19,
+     * exact) */
+    const float k32 = -1.9073486328125e-6f;
+    float u = sbyte(w.sc, 0) * fmaf(k32, xq.x, s0);
+    u = fmaf(sbyte(w.sc, 1), fmaf(k32, xq.y, s1), u);
+    u = fmaf(sbyte(w.sc, 2), fmaf(k32, xq.z, s2), u);
+    u = fmaf(sbyte(w.sc, 3), fmaf(k32, xq.w, s3), u);
+    return f16_bits_to_f32(w.dd) * 16777216.0f * u;
+}
+
+/* Lane item `it`'s 64 activations of a slice region (the layout above). */
+__device__ __forceinline__ void q6k_slice_x(const float4 *region, int it, float (&xv)[64])
+{
+    const int s = it >> 2, q = it & 3;
+    const int gbase = 64 * s + 32 * (q >> 1) + 4 * (q & 1);
+    /* slot (base | mix) ^ (8k + c): base and 8k + c share no bits */
+    const uint32_t off1 = (uint32_t)(gbase | q6k_slot_mix(gbase)) * 16u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 v = *(const float4 *)((const char *)region + (off1 ^ (16u * (8 * k + c))));
+            xv[16 * k + 4 * c] = v.x;
+            xv[16 * k + 4 * c + 1] = v.y;
+            xv[16 * k + 4 * c + 2] = v.z;
+            xv[16 * k + 4 * c + 3] = v.w;
+        }
+}
+
+/* SwiGLU workgroups hold at most 8 waves: the gate and up rows' sums then
+ * fit their registers (16-wave workgroups leave 128 per lane and spilled). */
+#define QMV_ROWLOOP_MAX_WAVES(EPI) ((EPI) == QMV_ROWDOT_SWIGLU ? 8 : 16)
+
+template <int NSL, int PD, int EPI>
+__global__ void __launch_bounds__(QMV_ROWLOOP_MAX_WAVES(EPI) * 64) rowloop_q6k_kernel(RowdotParams p)
+{
+    /* NSL slices of 1024 float4 (activations), then NSL x 64 float4 (run
+     * sums of each slice's items) */
+    extern __shared__ float4 q6k_xsh[];
+    float4 *const xqs = q6k_xsh + 1024 * NSL;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
+    const int sb = p.sb;
+    const float *const xp = p.x;
+    /* Job starts (first rows; unused slots start past every row), in one
+     * batch of scalar loads. */
+    int begin[QMV_MAX_JOBS];
+#pragma unroll
+    for (int i = 1; i < QMV_MAX_JOBS; ++i) begin[i] = p.job[i].wg_begin;
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* The activations into LDS: wave v copies slices v, v + nw, ...; chunks
+     * past the vector repeat its last chunk. */
+    const int last = 64 * sb - 1;
+    for (int sl = wave; sl < NSL; sl += nw) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int slot = 64 * k + lane;
+            const int g = min(1024 * sl + (slot ^ q6k_slot_mix(slot)), last);
+            __builtin_amdgcn_global_load_lds((const void *)((const float4 *)xp + g),
+                                             (lds_void *)(q6k_xsh + 1024 * sl + 64 * k), 16, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* This wave's row (global row index; past the launch's rows the wave
+     * only helps with the copies and, for the argmax, the candidates), its
+     * job and its first slice's weights. SwiGLU: the row of job 0 (gate),
+     * then the same row of job 1 (up). */
+    const int grow = (int)blockIdx.x * nw + wave;
+    const bool has_row = grow < p.groups;
+    int jj = 0;
+    if constexpr (EPI == QMV_ROWDOT_STORE) {
+#pragma unroll
+        for (int i = 1; i < QMV_MAX_JOBS; ++i) jj = grow >= begin[i] ? i : jj;
+    }
+    const RowdotJob &job = p.job[jj];
+    const int row = min(grow - job.wg_begin, job.rows - 1);
+    const size_t roff = (size_t)row * q6k_row_stride(sb);
+    gu8 *const rowp = (gu8 *)(uint64_t)job.w + roff;
+    gu8 *const rowp1 = EPI == QMV_ROWDOT_SWIGLU ? (gu8 *)(uint64_t)p.job[1].w + roff : rowp;
+    /* Slice j of a row has m super-blocks; lanes past 4 m repeat its last
+     * item. */
+    auto slice_m = [&](int j) { return min(16, sb - 16 * j); };
+    auto load_slice = [&](gu8 *rp, int j) {
+        const int m = slice_m(j);
+        return q6k_load_item(rp, j, m, min(lane, 4 * m - 1));
+    };
+    /* Slices j + 1 .. j + PD - 1 are in flight while slice j is computed
+     * (PD = 2: one slice ahead). */
+    constexpr int AHEAD = PD - 1 < NSL ? PD - 1 : NSL;
+    Q6Item wb[PD];
+#pragma unroll
+    for (int j = 0; j < AHEAD; ++j) wb[j] = load_slice(rowp, j);
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* This wave's copies (issued first) have landed once at most the
+     * weight loads issued after them are outstanding; then every wave's
+     * have, after the barrier. */
+    constexpr int VM = 5 * AHEAD;
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+    __builtin_amdgcn_s_barrier();
+    /* Run sums of every slice item: wave v for slices v, v + nw, ... */
+    for (int sl = wave; sl < NSL; sl += nw) {
+        float xv[64];
+        q6k_slice_x(q6k_xsh + 1024 * sl, min(lane, 4 * slice_m(sl) - 1), xv);
+        xqs[64 * sl + lane] = make_float4(quarter_sum(xv), quarter_sum(xv + 16), quarter_sum(xv + 32),
+                                          quarter_sum(xv + 48));
+    }
+    lds_barrier();
+    if (EPI != QMV_ROWDOT_ARGMAX && !has_row) return;
+
+    /* The row at rp: its slices in turn (slice 0's loads already issued),
+     * then the lane sums by DPP. */
+    auto row_total = [&](gu8 *rp) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NSL; ++j) {
+            const int m = slice_m(j), it = min(lane, 4 * m - 1);
+            if (j + AHEAD < NSL) wb[(j + AHEAD) % PD] = load_slice(rp, j + AHEAD);
+            float xv[64];
+            q6k_slice_x(q6k_xsh + 1024 * j, it, xv);
+            const float c = q6k_item_sum(wb[j % PD], xv, xqs[64 * j + lane]);
+            acc += lane < 4 * m ? c : 0.0f;
+        }
+        float tot[1];
+        segment_totals<64>(acc, tot);
+        return tot[0];
+    };
+    float out = 0.0f;
+    if (has_row) {
+        out = row_total(rowp);
+        if (job.add != nullptr) out += job.add[row];
+        if constexpr (EPI == QMV_ROWDOT_SWIGLU) {
+            /* the up row after the gate row (its first loads go out now) */
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < AHEAD; ++j) wb[j] = load_slice(rowp1, j);
+            float up = row_total(rowp1);
+            if (p.job[1].add != nullptr) up += p.job[1].add[row];
+            if (lane == 0) job.y[row] = swiglu_value(out, up);
+        } else {
+            if (lane == 0) job.y[row] = out;
+        }
+    }
+    if constexpr (EPI == QMV_ROWDOT_ARGMAX) {
+        /* One candidate per workgroup: the waves' rows meet in LDS and wave
+         * 0 publishes their merge. */
+        __shared__ uint64_t wcand[16];
+        float v;
+        int i, bad;
+        wave_candidate(has_row && lane == 0, row, out, v, i, bad);
+        if (lane == 0) wcand[wave] = pack_candidate(v, i, bad);
+        __syncthreads();
+        if (wave != 0) return;
+        float bv = -INFINITY;
+        int bi = 0x7fffffff, bb = 0;
+        for (int w = 0; w < nw; ++w) {
+            const uint64_t c = wcand[w];
+            const uint32_t hi = (uint32_t)(c >> 32);
+            bb |= (int)(hi >> 31);
+            argmax_merge(bv, bi, __uint_as_float((uint32_t)c), (int)(hi & 0x7fffffffu));
+        }
+        publish_tile_candidate(p, (int)blockIdx.x, bv, bi, bb, lane);
+    }
+}
+
 /* ---- host-side launchers -------------------------------------------------- */
 
 /* The tiled kernels pick a workgroup's job among all QMV_MAX_JOBS slots
@@ -3340,6 +3626,43 @@ hipError_t launch_rowgroup(const RowdotParams &p, int rows, int seg, int epi, in
 #undef QMV_ROWGROUP_N
 #undef QMV_ROWGROUP
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_rowloop_q6k(const RowdotParams &p, int epi, int grid, int waves, hipStream_t s)
+{
+    const int nsl = (p.sb + 15) / 16;
+    if (p.sb <= 16 || nsl > 8 || waves < 1 || waves > QMV_ROWLOOP_MAX_WAVES(epi) || grid < 1 ||
+        (long long)grid * waves < p.groups || (long long)(grid - 1) * waves >= p.groups)
+        return hipErrorInvalidValue;
+    if (p.njobs < 1 || p.njobs > QMV_MAX_JOBS) return hipErrorInvalidValue;
+    RowdotParams q = p;
+    for (int i = q.njobs; i < QMV_MAX_JOBS; ++i) q.job[i].wg_begin = INT_MAX;
+    const size_t lds = (size_t)nsl * (1024 + 64) * 16;
+    if ((epi == QMV_ROWDOT_SWIGLU && (p.njobs != 2 || p.job[1].rows != p.job[0].rows)) ||
+        (epi == QMV_ROWDOT_ARGMAX && (p.njobs != 1 || p.argmax_tiles != grid)))
+        return hipErrorInvalidValue;
+    switch (nsl * 4 + epi) {
+#define QMV_ROWLOOP_Q6(N, E)                                                                       \
+    case N * 4 + E: hipLaunchKernelGGL((rowloop_q6k_kernel<N, 2, E>), dim3(grid), dim3(waves * 64), lds, s, q); break;
+#define QMV_ROWLOOP_Q6E(N) QMV_ROWLOOP_Q6(N, QMV_ROWDOT_STORE) QMV_ROWLOOP_Q6(N, QMV_ROWDOT_SWIGLU) \
+    QMV_ROWLOOP_Q6(N, QMV_ROWDOT_ARGMAX)
+        QMV_ROWLOOP_Q6E(2) QMV_ROWLOOP_Q6E(3) QMV_ROWLOOP_Q6E(4) QMV_ROWLOOP_Q6E(5) QMV_ROWLOOP_Q6E(6)
+        QMV_ROWLOOP_Q6E(7) QMV_ROWLOOP_Q6E(8)
+#undef QMV_ROWLOOP_Q6E
+#undef QMV_ROWLOOP_Q6
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rowmajor_q6k(const uint8_t *raw, uint8_t *out, int rows, int sb, hipStream_t s)
+{
+    const long long total = (long long)rows * sb * 210;
+    const int threads = 256;
+    const long long grid = (total + threads - 1) / threads;
+    if (rows < 1 || sb < 1 || grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rowmajor_q6k_kernel, dim3((unsigned)grid), dim3(threads), 0, s, raw, out, sb, total);
+    return hipGetLastError();
 }
 
 hipError_t launch_dequant(int fmt, const uint8_t *w, float *out, int rows, int cols, int units,

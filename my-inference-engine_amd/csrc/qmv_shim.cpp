@@ -48,7 +48,7 @@ struct QmvDeviceTensor {
     int units, tiles;
     uint64_t packed_bytes, device_bytes;
     uint8_t *data;
-    uint8_t *rowmajor; /* Q4_K: the GGUF bytes as well (row-major kernel), else null */
+    uint8_t *rowmajor; /* row-major copy (Q4_K: the GGUF bytes; Q6_K: planes), else null */
 };
 
 namespace {
@@ -524,6 +524,19 @@ constexpr int kRowdotRowsLarge = 4;
  * at 4 and 19.1 at 1. A row's sum does not depend on the rows per segment,
  * so the fused result stays that of the plain launch's rows bit for bit. */
 constexpr int kRowdotRowsLargeSwiglu = 2;
+/* Q6_K rows of 17 to kRowdotMaxSb super-blocks keep a row-major copy in the
+ * chunked plane layout of rowloop_q6k_kernel (q6k_row_stride bytes per row)
+ * and run their single-position launches there (QMV_ROWDOT_Q6K = 0 at
+ * start-up keeps them tiled): one row per wave, workgroups of
+ * ceil(rows / kRowloopQ6Groups) waves (at most 16), each copying the
+ * activations into LDS once. Measured on MI355X, Qwen2.5-7B down
+ * (3584 x 18944), us per launch: 14.2 with 224 workgroups of 16 waves, 15.0
+ * with 256 of 14, 15.7 with 512 of 7, against 14.4-14.6 tiled; loading two
+ * or three slices ahead instead of one, 15.0 and 16.0. In the decode set's
+ * graph the step went 1.128 -> 1.108 ms (no split-K tail before the next
+ * launch). */
+std::atomic<int> g_rowdot_q6{env_int("QMV_ROWDOT_Q6K", 1)};
+constexpr long long kRowloopQ6Groups = 224;
 
 long long tiled_units(int rows, int blocks_per_row)
 {
@@ -533,7 +546,9 @@ long long tiled_units(int rows, int blocks_per_row)
 /* Whether an upload also keeps the GGUF bytes for the row-major kernel. */
 bool keeps_rowmajor(const QmvGeometry &geo, int rows, int blocks_per_row)
 {
-    return g_rowdot.load() != 0 && geo.format == QMV_FMT_Q4_K && blocks_per_row <= kRowdotMaxSb &&
+    if (g_rowdot.load() == 0 || blocks_per_row > kRowdotMaxSb) return false;
+    if (geo.format == QMV_FMT_Q6_K) return g_rowdot_q6.load() != 0 && blocks_per_row > kRowdotSharedSb;
+    return geo.format == QMV_FMT_Q4_K &&
            (tiled_units(rows, blocks_per_row) <= kRowdotMaxUnits || blocks_per_row <= kRowdotSharedSb);
 }
 
@@ -580,8 +595,17 @@ int tensor_upload(const QmvTensorView *m, const Shape &s, int device, hipStream_
                                s.geo.blocks_per_unit, s.geo.block_bytes, s.geo.unit_bytes, t->tiles, stream));
     HIP_TRY(hipStreamSynchronize(stream));
     if (keeps_rowmajor(s.geo, s.rows, s.blocks_per_row)) {
-        t->rowmajor = raw_guard.release();
-        t->device_bytes += t->packed_bytes;
+        if (s.geo.format == QMV_FMT_Q6_K) {
+            const uint64_t bytes = (uint64_t)s.rows * qmv::q6k_row_stride(s.blocks_per_row);
+            HIP_TRY(counted_malloc((void **)&t->rowmajor, bytes));
+            HIP_TRY(hipMemsetAsync(t->rowmajor, 0, bytes, stream));
+            HIP_TRY(qmv::launch_rowmajor_q6k(raw, t->rowmajor, s.rows, s.blocks_per_row, stream));
+            HIP_TRY(hipStreamSynchronize(stream));
+            t->device_bytes += bytes;
+        } else {
+            t->rowmajor = raw_guard.release();
+            t->device_bytes += t->packed_bytes;
+        }
     }
     *out = t.release();
     return 1;
@@ -836,10 +860,62 @@ struct ChunkPlan {
     size_t argmax_tiles = 0;               /* fused argmax candidate slots needed (0: none) */
 };
 
-/* A single-position launch of Q4_K tensors on the row-major kernel: every
- * tensor keeps its GGUF bytes, rows fit 8 waves of 16 super-blocks (one
- * wave's segment in launches of more than kRowdotMaxUnits pairs), and the
- * epilogue is at most an added vector, SwiGLU or the fused argmax. */
+/* A single-position launch on a row-major kernel: every tensor keeps a
+ * row-major copy and has the format of the first. Q4_K: rows fit 8 waves of
+ * 16 super-blocks (one wave's segment in launches of more than
+ * kRowdotMaxUnits pairs), and the epilogue is at most an added vector,
+ * SwiGLU, the fused argmax or the fused norm. Q6_K (rows of 17 to 128
+ * super-blocks): an added vector, SwiGLU or the fused argmax. */
+/* The Q6_K part of plan_rowdot (tensors checked there). */
+bool plan_rowdot_q6k(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
+                     const Epilogue &epi, ChunkPlan *cp)
+{
+    const QmvDeviceTensor *t0 = ts[0];
+    if (epi.norm_w) return false;
+    if (epi.swiglu && (count != 2 || ts[1]->rows != t0->rows)) return false; /* rejected by the tiled plan */
+    if (epi.argmax && (count != 1 || b0 != 0)) return false;
+    const int sb = t0->blocks_per_row;
+    if (sb <= kRowdotSharedSb || sb > kRowdotMaxSb) return false;
+    qmv::RowdotParams &rp = cp->rp;
+    memset(&rp, 0, sizeof rp);
+    rp.njobs = count;
+    rp.x = d_in + (size_t)b0 * t0->cols;
+    rp.sb = sb;
+    long long total = 0;
+    for (int i = 0; i < count; ++i) {
+        qmv::RowdotJob &j = rp.job[i];
+        j.w = ts[i]->rowmajor;
+        j.y = d_out[i] + (size_t)b0 * ts[i]->rows;
+        j.rows = ts[i]->rows;
+        j.wg_begin = (int)total;
+        if (epi.add && epi.add[i]) j.add = epi.add[i] + (size_t)b0 * epi.ldadd[i];
+        if (!epi.swiglu || i == 0) total += ts[i]->rows; /* SwiGLU: each wave takes a gate row and its up row */
+    }
+    if (total > INT_MAX) return false;
+    rp.groups = (int)total;
+    const int waves = (int)std::min<long long>(epi.swiglu ? 8 : 16, (total + kRowloopQ6Groups - 1) / kRowloopQ6Groups);
+    memset(&cp->p, 0, sizeof cp->p);
+    cp->rowdot = true;
+    cp->rd_rows = 1;
+    cp->rd_seg = 64;
+    cp->rd_epi = epi.swiglu ? QMV_ROWDOT_SWIGLU : epi.argmax ? QMV_ROWDOT_ARGMAX : QMV_ROWDOT_STORE;
+    cp->rd_norm = false;
+    cp->prefill = cp->paired = false;
+    cp->mt = 1;
+    cp->grid = (int)((total + waves - 1) / waves);
+    cp->waves = waves;
+    cp->fmt = QMV_FMT_Q6_K;
+    cp->partials = cp->counters = 0;
+    cp->pair_vals = cp->pair_count = 0;
+    /* Fused argmax candidates: one per workgroup. */
+    cp->argmax_tiles = epi.argmax ? (size_t)cp->grid : 0;
+    if (epi.argmax) {
+        rp.argmax_result = epi.argmax;
+        rp.argmax_tiles = cp->grid;
+    }
+    return true;
+}
+
 bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
                  const Epilogue &epi, ChunkPlan *cp)
 {
@@ -849,9 +925,11 @@ bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b
     const QmvDeviceTensor *t0 = ts[0];
     long long units = 0;
     for (int i = 0; i < count; ++i) {
-        if (ts[i]->rowmajor == nullptr || ts[i]->cols != t0->cols) return false;
+        if (ts[i]->rowmajor == nullptr || ts[i]->cols != t0->cols || ts[i]->geo.format != t0->geo.format)
+            return false;
         units += tiled_units(ts[i]->rows, ts[i]->blocks_per_row);
     }
+    if (t0->geo.format == QMV_FMT_Q6_K) return plan_rowdot_q6k(ts, count, d_in, b0, d_out, epi, cp);
     /* Large launches: rows of at most kRowdotSharedSb super-blocks, and no
      * fused argmax (a candidate per 16-row workgroup publishes four times as
      * often as the tiled kernel's 64-row tiles: 151936 x 3584 Q4_K took 98 us
@@ -1096,7 +1174,9 @@ void bind_workspace(ChunkPlan &cp, float *partials, unsigned *counters)
 
 int enqueue_chunk(const ChunkPlan &cp, hipStream_t stream)
 {
-    if (cp.rowdot)
+    if (cp.rowdot && cp.fmt == QMV_FMT_Q6_K)
+        HIP_TRY(qmv::launch_rowloop_q6k(cp.rp, cp.rd_epi, cp.grid, cp.waves, stream));
+    else if (cp.rowdot)
         HIP_TRY(qmv::launch_rowgroup(cp.rp, cp.rd_rows, cp.rd_seg, cp.rd_epi, cp.grid, cp.waves, stream, cp.rd_norm));
     else if (cp.prefill)
         HIP_TRY(qmv::launch_prefill(cp.fmt, cp.p, cp.mt, cp.grid, stream));

@@ -154,13 +154,18 @@ def test_reserve_rejects_bad_arguments(qmv, gpu):
 
 
 def test_graph_survives_workspace_growth(qmv, gpu, hip):
-    """Capture a split-K launch (Q6_K 3584 x 18944 at M = 1: 56 tiles in 13
-    K-splits) on a fresh stream, then run a 32-position launch of the same
-    tensor eagerly on that stream (its workspace grows past the captured
-    one), then replay: the replays still match the eager M = 1 bits."""
+    """Capture a split-K launch (Q6_K 3584 x 18944 at M = 1, uploaded with the
+    row-major kernels off so it runs tiled: 56 tiles in 13 K-splits) on a
+    fresh stream, then run a 32-position launch of the same tensor eagerly on
+    that stream (its workspace grows past the captured one), then replay:
+    the replays still match the eager M = 1 bits."""
     rows, cols = 3584, 18944
     big = qmv.synth_tensor(B.Q6_K, rows, cols, seed=72)
-    db = qmv.DeviceTensor(qmv.make_view(big, B.Q6_K, rows, cols))
+    qmv.set_rowmajor(False, 2)
+    try:
+        db = qmv.DeviceTensor(qmv.make_view(big, B.Q6_K, rows, cols))
+    finally:
+        qmv.set_rowmajor(True, 2)
     x = qmv.synth_normal(32 * cols, seed=73)
     dx = hip.DeviceBuffer.from_array(x)
     dy = hip.DeviceBuffer(4 * rows)

@@ -1,5 +1,5 @@
-"""GPU parity of the row-major single-position kernel (small Q4_K launches),
-through the C ABI.
+"""GPU parity of the row-major single-position kernels (Q4_K, and Q6_K rows
+of 17 to 128 super-blocks), through the C ABI.
 
 Q4_K tensors whose tiled plan covers at most 2048 (64-row tile, 256-weight
 unit) pairs keep their GGUF bytes on the device as well, and their
@@ -22,6 +22,12 @@ row segment (qmv_set_rowmajor). The bars are those of the tiled path:
     sampler (src/sampler.cpp:29-51);
   * with the row-major kernel switched off, new tensors keep no GGUF copy and
     run tiled, within the same bar.
+Q6_K tensors whose rows hold 17 to 128 super-blocks keep a copy in a
+chunked plane layout (210 bytes per super-block, rows padded to 16 bytes)
+and run their single-position launches on rowloop_q6k_kernel (one row per
+wave, taken in slices of 16 super-blocks, one 64-weight item per lane; a
+launch's rows, over several tensors, fill workgroups of up to 16 waves); the
+same row bar, addend and repeatability checks apply.
 """
 import os
 
@@ -86,9 +92,9 @@ def _device(qmv, rows, cols, seed):
     return raw, dt
 
 
-def _check(oracle, raw, rows, cols, x, y, what):
-    y_ref = oracle.matvec(raw, B.Q4_K, rows, cols, x)
-    _, absdot = oracle.row_stats(raw, B.Q4_K, rows, cols, x)
+def _check(oracle, raw, rows, cols, x, y, what, fmt=B.Q4_K):
+    y_ref = oracle.matvec(raw, fmt, rows, cols, x)
+    _, absdot = oracle.row_stats(raw, fmt, rows, cols, x)
     err = np.abs(y.astype(np.float64) - y_ref)
     bad = err > TOL * absdot
     assert not bad.any(), f"{what}: {int(bad.sum())} rows over tolerance"
@@ -332,3 +338,206 @@ def test_large_rowmajor_launches(qmv, oracle, gpu, hip, rows, cols):
         assert (np.abs(got - ref) <= SWIGLU_ULPS * 2.0 ** -23 * np.abs(ref) + 1e-30).all()
     dg.close()
     du.close()
+
+
+# ---- Q6_K ------------------------------------------------------------------
+
+def _q6_stride(sb):
+    return (210 * sb + 15) // 16 * 16
+
+
+def _device_q6(qmv, rows, cols, seed):
+    raw = qmv.synth_tensor(B.Q6_K, rows, cols, seed=seed)
+    dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q6_K, rows, cols))
+    sb = cols // 256
+    tiled = -(-rows // 64) * sb * 64 * 210
+    copy = rows * _q6_stride(sb) if 16 < sb <= 128 else 0
+    assert dt.device_bytes == tiled + copy, (rows, cols, dt.device_bytes)
+    return raw, dt
+
+
+# rows: one row, odd counts (workgroups with missing rows), tile edges, the
+# Qwen2.5-7B down projection (3584 x 18944); K: 17 (two waves, most lanes of
+# the second idle), 19, 33, 74, 100 and 128 super-blocks (8 full waves).
+Q6_SHAPES = [(1, 17 * 256), (2, 17 * 256), (5, 19 * 256), (63, 19 * 256), (65, 33 * 256), (130, 74 * 256),
+             (7, 100 * 256), (1, 128 * 256), (129, 128 * 256), (3584, 74 * 256)]
+
+
+@pytest.mark.parametrize("rows,cols", Q6_SHAPES)
+def test_rowmajor_q6k_matches_oracle(qmv, oracle, gpu, hip, rows, cols):
+    log(f"row-major Q6_K {rows}x{cols}")
+    raw, dt = _device_q6(qmv, rows, cols, seed=800 + rows + cols // 256)
+    x = qmv.synth_normal(cols, seed=801 + rows)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(4 * rows)
+    with hip.Stream() as s:
+        dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+        s.synchronize()
+        y = dy.to_array(np.float32, (rows,))
+        worst = _check(oracle, raw, rows, cols, x, y, f"Q6_K {rows}x{cols}", fmt=B.Q6_K)
+        for _ in range(2):
+            dy.fill(0)
+            dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+            s.synchronize()
+            assert np.array_equal(_bits(dy.to_array(np.float32, (rows,))), _bits(y))
+    log(f"  worst err/sum|wx| = {worst:.2e}")
+    dt.close()
+
+
+def test_rowmajor_q6k_group_and_addend(qmv, oracle, gpu, hip):
+    """Three Q6_K tensors over one input in one launch (3584, 100 and 1 rows
+    of 74 super-blocks): each within the bar and equal to its own launch bit
+    for bit; with addends, equal to those rows plus the addend."""
+    cols = 74 * 256
+    specs = [(3584, 810), (100, 811), (1, 812)]
+    tensors = [_device_q6(qmv, r, cols, seed) for r, seed in specs]
+    x = qmv.synth_normal(cols, seed=813)
+    dx = hip.DeviceBuffer.from_array(x)
+    outs = [hip.DeviceBuffer(4 * r) for r, _ in specs]
+    adds = [qmv.synth_normal(r, seed=814 + i) for i, (r, _) in enumerate(specs)]
+    dadds = [hip.DeviceBuffer.from_array(a) for a in adds]
+    sums = [hip.DeviceBuffer(4 * r) for r, _ in specs]
+    with hip.Stream() as s:
+        qmv.device_matvec_group([dt for _, dt in tensors], dx.ptr, 1, [o.ptr for o in outs], s.handle)
+        qmv.device_matvec_add_group([dt for _, dt in tensors], dx.ptr, 1, [d.ptr for d in dadds],
+                                    [0] * len(specs), [o.ptr for o in sums], s.handle)
+        s.synchronize()
+        for (raw, dt), (r, _), o, a, sm in zip(tensors, specs, outs, adds, sums):
+            y = o.to_array(np.float32, (r,))
+            _check(oracle, raw, r, cols, x, y, f"Q6_K group {r}x{cols}", fmt=B.Q6_K)
+            alone = hip.DeviceBuffer(4 * r)
+            dt.matvec(dx.ptr, 1, alone.ptr, s.handle)
+            s.synchronize()
+            assert np.array_equal(_bits(alone.to_array(np.float32, (r,))), _bits(y))
+            assert np.array_equal(_bits(sm.to_array(np.float32, (r,))), _bits(y + a))
+    for _, dt in tensors:
+        dt.close()
+
+
+def test_rowmajor_q6k_copy_policy(qmv, oracle, gpu, hip):
+    """Q6_K rows of at most 16 super-blocks (896 x 3584) keep no copy; with the
+    row-major kernels switched off, long rows keep none either; both run
+    tiled within the bar, and two positions of a tensor with a copy run
+    tiled within it too."""
+    raw, dt = _device_q6(qmv, 896, 3584, seed=820)
+    assert dt.device_bytes == 14 * 14 * 64 * 210
+    x = qmv.synth_normal(3584, seed=821)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(4 * 896)
+    with hip.Stream() as s:
+        dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+        s.synchronize()
+    _check(oracle, raw, 896, 3584, x, dy.to_array(np.float32, (896,)), "Q6_K short rows", fmt=B.Q6_K)
+    dt.close()
+    rows, cols = 200, 40 * 256
+    raw = qmv.synth_tensor(B.Q6_K, rows, cols, seed=822)
+    x2 = np.concatenate([qmv.synth_normal(cols, seed=823), qmv.synth_normal(cols, seed=824)])
+    dx = hip.DeviceBuffer.from_array(x2)
+    dy = hip.DeviceBuffer(4 * 2 * rows)
+    qmv.set_rowmajor(False, 2)
+    try:
+        dt = qmv.DeviceTensor(qmv.make_view(raw, B.Q6_K, rows, cols))
+        assert dt.device_bytes == 4 * 40 * 64 * 210
+        with hip.Stream() as s:
+            dt.matvec(dx.ptr, 1, dy.ptr, s.handle)
+            s.synchronize()
+        _check(oracle, raw, rows, cols, x2[:cols], dy.to_array(np.float32, (rows,)), "Q6_K switched off", fmt=B.Q6_K)
+        dt.close()
+    finally:
+        qmv.set_rowmajor(True, 2)
+    raw, dt = _device_q6(qmv, rows, cols, seed=822)
+    with hip.Stream() as s:
+        dt.matvec(dx.ptr, 2, dy.ptr, s.handle)
+        s.synchronize()
+    y = dy.to_array(np.float32, (2, rows))
+    for b in range(2):
+        _check(oracle, raw, rows, cols, x2[b * cols:(b + 1) * cols], y[b], f"Q6_K two positions, {b}", fmt=B.Q6_K)
+    dt.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 17 * 256), (65, 74 * 256), (300, 33 * 256), (130, 128 * 256)])
+def test_rowmajor_q6k_swiglu(qmv, oracle, gpu, hip, rows, cols):
+    """Fused SwiGLU over a Q6_K gate/up pair with long rows: within 4 ulp of
+    the oracle's transformer_swiglu_f32 of the plain launch's rows, which are
+    within the row bar."""
+    log(f"row-major Q6_K SwiGLU {rows}x{cols}")
+    raw_g, dg = _device_q6(qmv, rows, cols, 830)
+    raw_u, du = _device_q6(qmv, rows, cols, 831)
+    x = qmv.synth_normal(cols, seed=832)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        g = hip.DeviceBuffer(4 * rows)
+        u = hip.DeviceBuffer(4 * rows)
+        qmv.device_matvec_group([dg, du], dx.ptr, 1, [g.ptr, u.ptr], s.handle)
+        out = hip.DeviceBuffer(4 * rows)
+        qmv.device_matvec_swiglu(dg, du, dx.ptr, 1, out.ptr, s.handle)
+        s.synchronize()
+        gate, up = g.to_array(np.float32, (rows,)), u.to_array(np.float32, (rows,))
+        _check(oracle, raw_g, rows, cols, x, gate, "gate", fmt=B.Q6_K)
+        _check(oracle, raw_u, rows, cols, x, up, "up", fmt=B.Q6_K)
+        got = out.to_array(np.float32, (rows,)).astype(np.float64)
+        ok, ref = oracle.swiglu(gate, up)
+        assert ok == 1
+        ref = np.asarray(ref, dtype=np.float64)
+        assert (np.abs(got - ref) <= SWIGLU_ULPS * 2.0 ** -23 * np.abs(ref) + 1e-30).all()
+    dg.close()
+    du.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 17 * 256), (7, 74 * 256), (1000, 19 * 256), (3585, 74 * 256)])
+def test_rowmajor_q6k_fused_argmax(qmv, oracle, gpu, hip, rows, cols):
+    """Fused argmax over a Q6_K tensor with long rows (one candidate per
+    workgroup): logits bit-identical to the plain launch on every repeat, the
+    token the argmax of those logits, the logits within the row bar."""
+    log(f"row-major Q6_K fused argmax {rows}x{cols}")
+    raw, dt = _device_q6(qmv, rows, cols, 840 + rows)
+    x = qmv.synth_normal(cols, seed=841)
+    dx = hip.DeviceBuffer.from_array(x)
+    with hip.Stream() as s:
+        plain = hip.DeviceBuffer(4 * rows)
+        dt.matvec(dx.ptr, 1, plain.ptr, s.handle)
+        logits = hip.DeviceBuffer(4 * rows)
+        res = hip.DeviceBuffer(8)
+        for _ in range(3):  # the candidate counters must be left at zero
+            qmv.device_matvec_argmax(dt, dx.ptr, logits.ptr, res.ptr, s.handle)
+            s.synchronize()
+            y = logits.to_array(np.float32, (rows,))
+            assert np.array_equal(_bits(y), _bits(plain.to_array(np.float32, (rows,))))
+            token, finite = res.to_array(np.int32, (2,))
+            assert finite == 1 and token == int(np.argmax(y)), (token, int(np.argmax(y)))
+        _check(oracle, raw, rows, cols, x, y, "Q6_K logits", fmt=B.Q6_K)
+    dt.close()
+
+
+def test_rowmajor_q6k_argmax_ties_and_non_finite(qmv, gpu, hip):
+    """All-zero input: every logit is 0 and the lowest id wins. A row whose
+    first super-block has an infinite d gives a non-finite logit: token -1
+    and flag 0."""
+    rows, cols = 500, 40 * 256
+    raw = qmv.synth_tensor(B.Q6_K, rows, cols, seed=850)
+
+    def fused(buf, x):
+        dt = qmv.DeviceTensor(qmv.make_view(buf, B.Q6_K, rows, cols))
+        assert dt.device_bytes == 8 * 40 * 64 * 210 + rows * _q6_stride(40)
+        dx = hip.DeviceBuffer.from_array(x)
+        logits = hip.DeviceBuffer(4 * rows)
+        res = hip.DeviceBuffer(8)
+        with hip.Stream() as s:
+            out = []
+            for _ in range(2):
+                qmv.device_matvec_argmax(dt, dx.ptr, logits.ptr, res.ptr, s.handle)
+                s.synchronize()
+                out.append(res.to_array(np.int32, (2,)).tolist())
+        y = logits.to_array(np.float32, (rows,))
+        dt.close()
+        return out, y
+
+    out, y = fused(raw, np.zeros(cols, dtype=np.float32))
+    assert out == [[0, 1]] * 2 and not y.any()
+    bad = raw.copy()
+    row = rows - 3
+    off = row * 40 * 210 + 208  # d of the row's first super-block
+    bad[off:off + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), dtype=np.uint8)
+    out, y = fused(bad, qmv.synth_normal(cols, seed=851))
+    assert not np.isfinite(y[row]) and np.isfinite(np.delete(y, row)).all()
+    assert out == [[-1, 0]] * 2
