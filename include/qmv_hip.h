@@ -371,20 +371,24 @@ void qmv_set_launch_tuning(int target_waves, int units_per_wave,
                            int waves_per_group, int mfma_min_batch);
 
 /*
- * Row-major kernel for single-position Q4_K launches (process-wide; no
- * reference counterpart). A Q4_K tensor with at most 128 super-blocks per row
- * whose tiled layout holds at most 2048 (64-row tile, 256-weight unit) pairs,
- * or of any size with at most 16 super-blocks per row, keeps its GGUF bytes
- * on the device as well while enable != 0 (the default), and its
- * single-position launches read those (for a Qwen2.5-7B-shaped model: q, k,
- * v, o, gate and up, 92.9 MB per layer, 2.60 GB in all, +62.5% over the
- * packed weights). enable = 0 stops both for launches planned and tensors
+ * Row-major kernels for single-position Q4_K and Q6_K launches
+ * (process-wide; no reference counterpart). A Q4_K tensor with at most 128
+ * super-blocks per row whose tiled layout holds at most 2048 (64-row tile,
+ * 256-weight unit) pairs, or of any size with at most 16 super-blocks per
+ * row, keeps its GGUF bytes on the device as well while enable != 0 (the
+ * default), and a Q6_K tensor with 17 to 128 super-blocks per row keeps a
+ * row-major copy in chunks of 16 super-blocks (210 bytes per super-block,
+ * rows padded to 16 bytes); their single-position launches read those (for
+ * a Qwen2.5-7B-shaped model: q, k, v, o, gate and up, 92.9 MB per layer,
+ * and down, 55.7 MB: 4.16 GB in all, +100% over the packed weights, 2.9% of
+ * one GPU's HBM). enable = 0 stops both for launches planned and tensors
  * uploaded afterwards: memory-bound callers set it before loading the
  * weights. rows (1, 2 or 4; other values: 2) is how many rows each 64-lane
- * row segment takes in launches of at most 2048 pairs (larger launches take
- * 4, or 2 with the fused SwiGLU). QMV_ROWDOT=0 / QMV_ROWDOT_ROWS in the
- * environment set the same at start-up. Results stay within the row
- * tolerance either way.
+ * row segment of the Q4_K kernel takes in launches of at most 2048 pairs
+ * (larger launches take 4, or 2 with the fused SwiGLU). QMV_ROWDOT=0 /
+ * QMV_ROWDOT_ROWS in the environment set the same at start-up, and
+ * QMV_ROWDOT_Q6K=0 keeps Q6_K tensors tiled only. Results stay within the
+ * row tolerance either way.
  */
 void qmv_set_rowmajor(int enable, int rows);
 
