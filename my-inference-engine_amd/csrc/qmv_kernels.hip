@@ -3418,12 +3418,13 @@ __global__ void __launch_bounds__(QMV_ROWLOOP_MAX_WAVES(EPI) * 64) rowloop_q6k_k
     for (int i = 1; i < QMV_MAX_JOBS; ++i) begin[i] = p.job[i].wg_begin;
     __builtin_amdgcn_sched_barrier(0);
 
-    /* The activations into LDS: wave v copies slices v, v + nw, ...; chunks
-     * past the vector repeat its last chunk. */
+    /* The activations into LDS: every wave copies its share of every slice
+     * (1 KiB pieces k = v, v + nw, ... of slice 0, then of slice 1, ...);
+     * chunks past the vector repeat its last chunk. */
     const int last = 64 * sb - 1;
-    for (int sl = wave; sl < NSL; sl += nw) {
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
+    for (int sl = 0; sl < NSL; ++sl) {
+        for (int k = wave; k < 16; k += nw) {
             const int slot = 64 * k + lane;
             const int g = min(1024 * sl + (slot ^ q6k_slot_mix(slot)), last);
             __builtin_amdgcn_global_load_lds((const void *)((const float4 *)xp + g),
