@@ -534,7 +534,8 @@ constexpr int kRowdotRowsLargeSwiglu = 2;
  * with 256 of 14, 15.7 with 512 of 7, against 14.4-14.6 tiled; loading two
  * or three slices ahead instead of one, 15.0 and 16.0. In the decode set's
  * graph the step went 1.128 -> 1.108 ms (no split-K tail before the next
- * launch). */
+ * launch), 1.095-1.101 with every wave copying its share of the
+ * activations. */
 std::atomic<int> g_rowdot_q6{env_int("QMV_ROWDOT_Q6K", 1)};
 constexpr long long kRowloopQ6Groups = 224;
 
@@ -860,13 +861,8 @@ struct ChunkPlan {
     size_t argmax_tiles = 0;               /* fused argmax candidate slots needed (0: none) */
 };
 
-/* A single-position launch on a row-major kernel: every tensor keeps a
- * row-major copy and has the format of the first. Q4_K: rows fit 8 waves of
- * 16 super-blocks (one wave's segment in launches of more than
- * kRowdotMaxUnits pairs), and the epilogue is at most an added vector,
- * SwiGLU, the fused argmax or the fused norm. Q6_K (rows of 17 to 128
- * super-blocks): an added vector, SwiGLU or the fused argmax. */
-/* The Q6_K part of plan_rowdot (tensors checked there). */
+/* The Q6_K part of plan_rowdot (tensors checked there): rowloop_q6k_kernel,
+ * one row per wave (SwiGLU: a gate row and its up row). */
 bool plan_rowdot_q6k(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
                      const Epilogue &epi, ChunkPlan *cp)
 {
@@ -916,6 +912,12 @@ bool plan_rowdot_q6k(QmvDeviceTensor *const *ts, int count, const float *d_in, i
     return true;
 }
 
+/* A single-position launch on a row-major kernel: every tensor keeps a
+ * row-major copy and has the format of the first. Q4_K: rows fit 8 waves of
+ * 16 super-blocks (one wave's segment in launches of more than
+ * kRowdotMaxUnits pairs), and the epilogue is at most an added vector,
+ * SwiGLU, the fused argmax or the fused norm. Q6_K (rows of 17 to 128
+ * super-blocks): an added vector, SwiGLU or the fused argmax. */
 bool plan_rowdot(QmvDeviceTensor *const *ts, int count, const float *d_in, int b0, float *const *d_out,
                  const Epilogue &epi, ChunkPlan *cp)
 {
