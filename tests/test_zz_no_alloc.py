@@ -77,9 +77,12 @@ def test_two_calls_second_smaller(qmv, gpu, hip):
             d.close()
 
 
-@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 3584, 18944, 1), (B.Q5_0, 1536, 1536, 6),
-                                               (B.Q6_K, 896, 4864, 20), (B.Q4_K, 1000, 2304, 2)])
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 3584, 18944, 1), (B.Q6_K, 1000, 3584, 1),
+                                               (B.Q5_0, 1536, 1536, 6), (B.Q6_K, 896, 4864, 20),
+                                               (B.Q4_K, 1000, 2304, 2)])
 def test_formats_and_batches(qmv, gpu, hip, t, rows, cols, batch):
+    """Q6_K 3584 x 18944 at one position runs row-major (no scratch); Q6_K
+    1000 x 3584 (14 K-units, tiled) splits K at one position."""
     with hip.Stream() as stream:
         dts = _tensors(qmv, t, [rows], cols, seed=rows + batch)
         log(f"noalloc: {B.NAMES[t]} {rows}x{cols}, M={batch}")
@@ -110,14 +113,15 @@ def test_vocab_shape_and_oversized_call(qmv, gpu, hip):
         dts[0].close()
 
 
-@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 896, 4864, 1), (B.Q4_K, 3584, 3584, 8),
-                                               (B.Q4_K, 3584, 3584, 1)])
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 1000, 3584, 1), (B.Q4_K, 3584, 3584, 8),
+                                               (B.Q4_K, 3584, 3584, 1), (B.Q6_K, 896, 4864, 1)])
 def test_graph_capture_and_replays(qmv, gpu, hip, t, rows, cols, batch):
     """The call captured into a graph replays to the eager bits, with eager
-    work between replays. Q6_K 896 x 4864 at one position (19 K-units in 5
-    splits per tile) and Q4_K 3584 x 3584 at 8 positions split K, so their
+    work between replays. Q6_K 1000 x 3584 at one position (14 K-units,
+    tiled, in splits) and Q4_K 3584 x 3584 at 8 positions split K, so their
     counters live in the scratch array and are cleared by a fill-kernel node;
-    Q4_K 3584 x 3584 at one position runs row-major with no split."""
+    Q4_K 3584 x 3584 and Q6_K 896 x 4864 at one position run row-major with
+    no split."""
     with hip.Stream() as stream:
         dts = _tensors(qmv, t, [rows], cols, seed=550 + batch)
         x = qmv.synth_normal(batch * cols, seed=551)
