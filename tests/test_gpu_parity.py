@@ -519,12 +519,15 @@ def test_group_launch_matches_oracle(qmv, oracle, gpu, hip, shapes):
         d.close()
 
 
-@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 3584, 18944, 1), (B.Q4_K, 3584, 3584, 8),
-                                               (B.Q6_K, 896, 4864, 8), (B.Q4_K, 512, 3584, 3)])
+@pytest.mark.parametrize("t,rows,cols,batch", [(B.Q6_K, 3584, 18944, 1), (B.Q6_K, 1000, 3584, 1),
+                                               (B.Q4_K, 3584, 3584, 8), (B.Q6_K, 896, 4864, 8),
+                                               (B.Q4_K, 512, 3584, 3)])
 def test_graph_replays_match_eager(qmv, gpu, hip, t, rows, cols, batch):
     """A captured launch (split-K counters reset by the kernel itself, no
     memset nodes) replays to the eager result, with host work in between; at
-    M = 8 the launch runs on the matrix cores."""
+    M = 8 the launch runs on the matrix cores. Q6_K 3584 x 18944 at one
+    position runs row-major (no split); Q6_K 1000 x 3584 (14 K-units, tiled)
+    splits K at one position."""
     raw = qmv.synth_tensor(t, rows, cols, seed=61)
     dt = qmv.DeviceTensor(qmv.make_view(raw, t, rows, cols))
     x = qmv.synth_normal(batch * cols, seed=62)
