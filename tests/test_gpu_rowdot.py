@@ -357,10 +357,12 @@ def _device_q6(qmv, rows, cols, seed):
 
 
 # rows: one row, odd counts (workgroups with missing rows), tile edges, the
-# Qwen2.5-7B down projection (3584 x 18944); K: 17 (two waves, most lanes of
-# the second idle), 19, 33, 74, 100 and 128 super-blocks (8 full waves).
+# Qwen2.5-7B down projection (3584 x 18944), workgroups of 1..16 waves; K:
+# 17 (two slices, the second of one super-block), 19, 32 and 64 (whole last
+# slices), 33, 74, 100, 112 and 128 super-blocks (8 slices).
 Q6_SHAPES = [(1, 17 * 256), (2, 17 * 256), (5, 19 * 256), (63, 19 * 256), (65, 33 * 256), (130, 74 * 256),
-             (7, 100 * 256), (1, 128 * 256), (129, 128 * 256), (3584, 74 * 256)]
+             (7, 100 * 256), (1, 128 * 256), (129, 128 * 256), (3584, 74 * 256), (225, 32 * 256),
+             (3, 64 * 256), (449, 112 * 256)]
 
 
 @pytest.mark.parametrize("rows,cols", Q6_SHAPES)
