@@ -2027,14 +2027,32 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    /* Group c's codes load two steps before the step that converts them
+     * (step 2c - 1, below): group 1's here, groups 2 and 3 at steps 1 and
+     * 3, each into the buffer the group before last used. */
+    {
+        gu8 *nq = bytes_after(qsp + 2048, acc[0][1][0]);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) q[1][g] = gload8(nq + g * 256);
+    }
+    /* A software pipeline over the 8 sub-blocks: step sb issues its MFMAs,
+     * the code conversion of sub-block sb + 1 (b -> bn) and the scale FMAs
+     * of sub-block sb - 1 (dp, sp), none of which depends on the others, so
+     * the VALU work runs under the matrix-core work. acc takes the
+     * sub-blocks in order, as without the pipeline. */
+    bf16x8_t b[4], bn[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) b[g] = q4_codes_bf16(q[0][g].x, q[0][g].y, false);
+    f32x4_t dp[P][4];
+    float sp[4];
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
-        const int c = sb >> 1;
         const bool high = sb & 1;
-        if (!high && c + 1 < 4) {
-            gu8 *nq = bytes_after(qsp + (c + 1) * 2048, acc[0][1][0]);
+        if (high && (sb + 3) / 2 < 4) {
+            const int cn = (sb + 3) / 2;
+            gu8 *nq = bytes_after(qsp + cn * 2048, acc[0][1][0]);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) q[(c + 1) & 1][g] = gload8(nq + g * 256);
+            for (int g = 0; g < 4; ++g) q[cn & 1][g] = gload8(nq + g * 256);
         }
         if (sb == QMV_PF_NEXT_SB) {
             gu8 *np = bytes_after(next, acc[0][2][0]);
@@ -2044,11 +2062,19 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
                 qn[g] = gload8(np + qoff + g * 256);
             }
         }
-        bf16x8_t b[4];
+        if (sb + 1 < 8)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            b[g] = q4_codes_bf16(q[c & 1][g].x, q[c & 1][g].y, high);
+            for (int g = 0; g < 4; ++g)
+                bn[g] = q4_codes_bf16(q[((sb + 1) >> 1) & 1][g].x, q[((sb + 1) >> 1) & 1][g].y, !high);
         float sa[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint4 hg = h[g];
+            const float dd = f16_bits_to_f32(hg.x);
+            const uint32_t scw = sb < 4 ? hg.y & 0x3f3f3f3fu : (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
+            sa[g] = dd * ubyte(scw, sb & 3);
+        }
+        f32x4_t d[P][4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
             typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
@@ -2056,33 +2082,39 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
             const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, sb));
             const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, sb));
             const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, sb));
-            f32x4_t d[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int g = 0; g < 4; ++g) d[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[g], d[pb][g], 0, 0, 0);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[g], d[pb][g], 0, 0, 0);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[g], 0, 0, 0);
-            if (pb == 0) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const uint4 hg = h[g];
-                    const float dd = f16_bits_to_f32(hg.x);
-                    const uint32_t scw =
-                        sb < 4 ? hg.y & 0x3f3f3f3fu : (hg.w & 0x0f0f0f0fu) | ((hg.y >> 2) & 0x30303030u);
-                    sa[g] = dd * ubyte(scw, sb & 3);
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[pb][g][j] = fmaf(sa[g], d[g][j], acc[pb][g][j]);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[g], d[pb][g], 0, 0, 0);
         }
-        /* One sub-block's codes and scales live at a time. */
+        if (sb > 0)
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[pb][g][j] = fmaf(sp[g], dp[pb][g][j], acc[pb][g][j]);
+        /* One step per scheduling region: only the pipeline's hand-over
+         * values live across it. */
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            b[g] = bn[g];
+            sp[g] = sa[g];
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb) dp[pb][g] = d[pb][g];
+        }
     }
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[pb][g][j] = fmaf(sp[g], dp[pb][g][j], acc[pb][g][j]);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         h[g] = hn[g];
@@ -2111,6 +2143,31 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
         for (int e = 0; e < 3; ++e) w[0][g][e] = w0[g][e];
     uint4 scn[4];
     uint32_t dgn[4], wn[4][3];
+    /* Step t's code operands: one combined operand per code (q - 32, exact
+     * in bf16), converted once for every position block. The two-operand
+     * form of the M <= 8 kernel (q6_codes_bf16) would double the MFMAs of
+     * each block, and using it for one block only would make a position's
+     * rounding depend on the number of positions in its launch. */
+    auto decode = [&](int t, bf16x4_t (&b)[4]) {
+        const int pr = t >> 2, r = t & 3;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t lw = w[pr & 1][g][r & 1];
+            const uint32_t hw = w[pr & 1][g][2];
+            const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
+        }
+    };
+    /* A software pipeline over the 16 steps: step t issues its MFMAs, the
+     * code conversion of step t + 1 (b -> bn) and the scale FMAs of step
+     * t - 1 (dp, sp), none of which depends on the others, so the VALU work
+     * runs under the matrix-core work instead of before and after it. acc
+     * takes the steps in order, as without the pipeline. */
+    bf16x4_t b[4], bn[4];
+    decode(0, b);
+    f32x4_t dp[P][4];
+    float sp[4];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
         const int pr = t >> 2, r = t & 3;
@@ -2137,21 +2194,11 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
                 wn[g][2] = *(gu32 *)(np + woff + 8 * 1024 + g * 256);
             }
         }
-        /* One combined operand per code (q - 32, exact in bf16), converted
-         * once for every position block. The two-operand form of the M <= 8
-         * kernel (q6_codes_bf16) would double the MFMAs of each block, and
-         * using it for one block only would make a position's rounding depend
-         * on the number of positions in its launch. */
-        bf16x4_t b[4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t lw = w[pr & 1][g][r & 1];
-            const uint32_t hw = w[pr & 1][g][2];
-            const uint32_t c = codes(((lw >> (4 * (r >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * r)) & 0x03030303u) << 4));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) b[g][i] = (__bf16)(ubyte(c, i) - 32.0f); /* exact: -32..31 */
-        }
+        if (t + 1 < 16) decode(t + 1, bn);
         float s[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) s[g] = dg[g] * sbyte(word(sc[g], j >> 2), j & 3);
+        f32x4_t d[P][4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
             typedef __attribute__((address_space(3))) const bf16x4_t lds_a;
@@ -2159,26 +2206,39 @@ __device__ __forceinline__ void q6k_unit_pf(const uint8_t *slab, const uint8_t *
             const bf16x4_t a0 = *(lds_a *)(la + L::offset(0, pb, j));
             const bf16x4_t a1 = *(lds_a *)(la + L::offset(1, pb, j));
             const bf16x4_t a2 = *(lds_a *)(la + L::offset(2, pb, j));
-            f32x4_t d[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int g = 0; g < 4; ++g) d[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a0, b[g], d[pb][g], 0, 0, 0);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[g], 0, 0, 0);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a1, b[g], d[pb][g], 0, 0, 0);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) d[g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[g], 0, 0, 0);
-            if (pb == 0)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) s[g] = dg[g] * sbyte(word(sc[g], j >> 2), j & 3);
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(s[g], d[g][i], acc[pb][g][i]);
+            for (int g = 0; g < 4; ++g) d[pb][g] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a2, b[g], d[pb][g], 0, 0, 0);
         }
-        /* One sub-block's codes and scale live at a time. */
+        if (t > 0)
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(sp[g], dp[pb][g][i], acc[pb][g][i]);
+        /* One step per scheduling region: only the pipeline's hand-over
+         * values live across it. */
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            b[g] = bn[g];
+            sp[g] = s[g];
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb) dp[pb][g] = d[pb][g];
+        }
     }
+#pragma unroll
+    for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[pb][g][i] = fmaf(sp[g], dp[pb][g][i], acc[pb][g][i]);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         sc[g] = scn[g];
