@@ -83,6 +83,10 @@ struct MatvecParams {
      * (partials [tiles][splits][2][64] at job 0's offsets), so no second
      * count per tile pair is needed. */
     int pair_waves;
+    /* Prefill launches (set by launch_prefill): the splits publish their
+     * partials and stop, and a second kernel (pf_reduce_kernel) sums them and
+     * runs the epilogue; no arrival counts are taken. */
+    int pf_deferred;
 };
 
 /* One tensor of a row-major single-position launch: `w` holds the GGUF bytes
@@ -161,8 +165,10 @@ hipError_t launch_gather(int fmt, const uint8_t *w, const int *ids, int count, f
 hipError_t launch_repack(int fmt, const uint8_t *raw, uint8_t *out, int rows, int blocks_per_row,
                          int units, int blocks_per_unit, int block_bytes, int unit_bytes, int tiles,
                          hipStream_t s);
-/* Prefill launch (Q4_K / Q6_K, up to `rows` = 16 or 32 positions): grid =
- * sum over jobs of ceil(tiles / 4) tile groups x splits. */
+/* Prefill launch (up to `rows` = 16 or 32 positions): grid = sum over jobs
+ * of ceil(tiles / 4) tile groups x splits; for launches whose split-K finish
+ * would take QMV_PF_DEFER_ROUNDS or more rounds of partial loads, followed by
+ * the reduction kernel. */
 hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s);
 /* Plain fp32 copy (n elements) as a kernel, e.g. from mapped host memory. */
 hipError_t launch_copy(const float *src, float *dst, size_t n, hipStream_t s);

@@ -2479,6 +2479,8 @@ __device__ __forceinline__ void pf_finish(const MatvecParams &p, const WgWork &w
                                val[(4 * q + 3) * 64 + lane]};
             asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(mine + q * 256), "v"(v) : "memory");
         }
+        /* Deferred finish: pf_reduce_kernel, launched next, sums the tile. */
+        if (p.pf_deferred) return;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned prev = 0;
         if (lane == 0) prev = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3779,7 +3781,79 @@ hipError_t launch_argmax(const float *logits, int n, float *bval, int *bidx, int
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s)
+/* The deferred split-K finish of a prefill launch: thread (tile, quad q,
+ * lane) sums the quad of position rows 4q..4q+3 of row 64 tile + lane over
+ * the tile's splits, in split order as pf_finish does (so the values are
+ * those of the in-kernel finish bit for bit), with up to 8 splits' loads in
+ * flight at once, then applies pf_emit's addend and SwiGLU epilogues (the up
+ * sums of job 1 are read alongside, so no pairing protocol is needed). The
+ * partials were written by the previous kernel on this stream, whose end
+ * makes them visible: plain loads. */
+template <int MP>
+__global__ void __launch_bounds__(256) pf_reduce_kernel(MatvecParams p)
+{
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    const int lane = gid & 63;
+    const int q = (gid >> 6) % (MP / 4);
+    int t = (gid >> 6) / (MP / 4);
+    const int nj = p.swiglu ? 1 : p.njobs;
+    int j = 0;
+    while (j < nj && t >= p.job[j].tiles) {
+        t -= p.job[j].tiles;
+        ++j;
+    }
+    if (j >= nj) return;
+    const MatvecJob &job = p.job[j];
+    const int row = t * 64 + lane;
+    if (row >= job.rows) return;
+    const int S = job.splits;
+    auto total = [&](const MatvecJob &jb) {
+        const float *part = p.partials + jb.partial_offset + ((size_t)t * S) * MP * 64 + ((size_t)q * 64 + lane) * 4;
+        f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < S; s0 += 8) {
+            /* splits past the last repeat it and are not added */
+            f32x4_t v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *(const f32x4_t *)(part + (size_t)min(s0 + i, S - 1) * (MP / 4) * 256);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (s0 + i < S) sum = s0 + i == 0 ? v[i] : sum + v[i];
+        }
+        return sum;
+    };
+    const f32x4_t a = total(job);
+    const f32x4_t u = p.swiglu ? total(p.job[1]) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = 4 * q + e;
+        if (m >= p.positions) break;
+        float v = a[e];
+        if (job.add != nullptr) v += job.add[(size_t)m * job.ldadd + row];
+        if (p.swiglu) {
+            float w = u[e];
+            if (p.job[1].add != nullptr) w += p.job[1].add[(size_t)m * p.job[1].ldadd + row];
+            v = swiglu_value(v, w);
+        }
+        job.y[(size_t)m * job.ldy + row] = v;
+    }
+}
+
+/* Prefill launches whose in-kernel finish would take this many rounds of
+ * partial loads or more (ceil(splits / (64 / rows)); 16 quads per round)
+ * finish in pf_reduce_kernel instead. Measured on MI355X (µs per launch,
+ * Qwen2.5-7B layer shapes, cold graphs of 28, in-kernel / deferred): at 32
+ * positions q|k|v (14 splits, 7 rounds) 18.5 / 16.3, o (7 rounds) 17.5 /
+ * 14.4, down (15 splits, 8 rounds) 46.3 / 44.5, gate|up (3 splits, 2 rounds)
+ * 47.8 / 49.6; at 16 positions q|k|v (4 rounds) 13.3 / 12.3, o 12.4 / 11.1,
+ * down (4 rounds) 35.0 / 35.4, gate|up (1 round) 33.1 / 35.8. In the
+ * decode-step set (same box) deferring the launches of 4 rounds or more gave
+ * 3.513 against 3.655 ms at 32 positions but 2.612 against 2.600 at 16, so
+ * the 4-round launches keep the in-kernel finish. */
+#ifndef QMV_PF_DEFER_ROUNDS
+#define QMV_PF_DEFER_ROUNDS 5
+#endif
+
+static hipError_t launch_prefill_kernel(int fmt, const MatvecParams &p, int rows, int grid, hipStream_t s)
 {
     const dim3 g(grid), b(QMV_PF_WAVES * 64);
     if (fmt == QMV_FMT_Q4_K && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q4_K, 1>), g, b, 0, s, p);
@@ -3791,6 +3865,23 @@ hipError_t launch_prefill(int fmt, const MatvecParams &p, int rows, int grid, hi
     else if (fmt == QMV_FMT_Q8_0 && rows == 16) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q8_0, 1>), g, b, 0, s, p);
     else if (fmt == QMV_FMT_Q8_0 && rows == 32) hipLaunchKernelGGL((prefill_kernel<QMV_FMT_Q8_0, 2>), g, b, 0, s, p);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(int fmt, const MatvecParams &params, int rows, int grid, hipStream_t s)
+{
+    if (rows != 16 && rows != 32) return hipErrorInvalidValue;
+    MatvecParams p = params;
+    const int S = p.job[0].splits, per_round = 64 / rows;
+    p.pf_deferred = S > 1 && (S + per_round - 1) / per_round >= QMV_PF_DEFER_ROUNDS ? 1 : 0;
+    const hipError_t e = launch_prefill_kernel(fmt, p, rows, grid, s);
+    if (e != hipSuccess || !p.pf_deferred) return e;
+    long long tiles = 0;
+    for (int j = 0; j < (p.swiglu ? 1 : p.njobs); ++j) tiles += p.job[j].tiles;
+    const long long threads = tiles * (rows / 4) * 64;
+    const dim3 rg((unsigned)((threads + 255) / 256)), rb(256);
+    if (rows == 16) hipLaunchKernelGGL((pf_reduce_kernel<16>), rg, rb, 0, s, p);
+    else hipLaunchKernelGGL((pf_reduce_kernel<32>), rg, rb, 0, s, p);
     return hipGetLastError();
 }
 

@@ -79,9 +79,11 @@ def test_prefill_32_at_layer_shapes(qmv, oracle, gpu, t, rows, cols):
 @pytest.mark.parametrize("batch", [16, 27, 32])
 def test_prefill_long_rows_q5_q8(qmv, oracle, gpu, t, rows, cols, batch):
     """Q8_0 / Q5_0 prefill launches over rows of 32 or more four-block units
-    (K >= 4096), where the plan takes three units per split for launches of
-    at most 8 tile groups and five otherwise; two shapes end in a partial
-    last unit (131 and 133 blocks)."""
+    (K >= 4096), where the plan takes two units per split for launches of at
+    most 8 tile groups and five otherwise; two shapes end in a partial last
+    unit (131 and 133 blocks). The first two shapes split K 19 and 35 ways, so
+    their launches finish in the reduction kernel (pf_reduce_kernel) at every
+    batch here, 16 position rows included."""
     raw = qmv.synth_tensor(t, rows, cols, seed=340 + batch)
     x = qmv.synth_normal(batch * cols, seed=341 + batch).reshape(batch, cols)
     v = qmv.make_view(raw, t, rows, cols)
