@@ -121,10 +121,18 @@ def test_prefill_positions_independent(qmv, gpu, hip, t, batch, parts):
     dt.close()
 
 
-def test_prefill_epilogues(qmv, oracle, gpu, hip):
-    """Bias addend and fused SwiGLU on a 32-position launch (the positions
-    past the batch inside the kernel's position block are never stored)."""
-    t, rows, cols, batch = B.Q4_K, 1000, 3584, 27
+@pytest.mark.parametrize("cols,batch", [(3584, 27), (1024, 27), (7936, 12), (3584, 12)],
+                         ids=["32rows-reduction-kernel", "32rows-in-kernel", "16rows-reduction-kernel",
+                              "16rows-in-kernel"])
+def test_prefill_epilogues(qmv, oracle, gpu, hip, cols, batch):
+    """Bias addend and fused SwiGLU on prefill launches (the positions past
+    the batch inside the kernel's position blocks are never stored), for both
+    split-K finishes: in the reduction kernel (pf_reduce_kernel) where the
+    in-kernel finish would take 5 or more rounds of partial loads (K = 3584:
+    14 splits at 32 position rows, 7 rounds; K = 7936: 31 splits at 16, 8
+    rounds), and inside the prefill kernel with its SwiGLU pair protocol
+    otherwise (K = 1024: 4 splits; K = 3584 at 16 position rows: 4 rounds)."""
+    t, rows = B.Q4_K, 1000
     raw_g = qmv.synth_tensor(t, rows, cols, seed=330)
     raw_u = qmv.synth_tensor(t, rows, cols, seed=331)
     dg = qmv.DeviceTensor(qmv.make_view(raw_g, t, rows, cols))
@@ -139,7 +147,7 @@ def test_prefill_epilogues(qmv, oracle, gpu, hip):
     gate = g.to_array(np.float32, (batch + 5, rows))
     assert np.all(_bits(gate[batch:]) == 0x7f7f7f7f)
     gate, up = gate[:batch], u.to_array(np.float32, (batch, rows))
-    _check(oracle, raw_g, t, rows, cols, x, gate, "gate B=27")
+    _check(oracle, raw_g, t, rows, cols, x, gate, f"gate B={batch}")
     bias = np.random.default_rng(333).standard_normal(rows).astype(np.float32)
     db = hip.DeviceBuffer.from_array(bias)
     out = hip.DeviceBuffer(4 * batch * rows)
