@@ -82,7 +82,9 @@ def test_two_calls_second_smaller(qmv, gpu, hip):
                                                (B.Q4_K, 1000, 2304, 2)])
 def test_formats_and_batches(qmv, gpu, hip, t, rows, cols, batch):
     """Q6_K 3584 x 18944 at one position runs row-major (no scratch); Q6_K
-    1000 x 3584 (14 K-units, tiled) splits K at one position."""
+    1000 x 3584 (14 K-units, tiled) splits K at one position; Q6_K 896 x 4864
+    at 20 positions splits K 19 ways and finishes in the prefill reduction
+    kernel, whose partials live in the scratch array too."""
     with hip.Stream() as stream:
         dts = _tensors(qmv, t, [rows], cols, seed=rows + batch)
         log(f"noalloc: {B.NAMES[t]} {rows}x{cols}, M={batch}")
