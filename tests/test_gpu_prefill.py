@@ -165,6 +165,34 @@ def test_prefill_epilogues(qmv, oracle, gpu, hip, cols, batch):
     du.close()
 
 
+@pytest.mark.parametrize("t", [B.Q4_K, B.Q6_K])
+@pytest.mark.parametrize("batch", [27, 32])
+def test_prefill_group_of_unequal_tensors(qmv, oracle, gpu, hip, t, batch):
+    """A grouped launch of three tensors of unequal rows (17, 2 and 1 tiles,
+    the last two partial) over K = 3584 (14 splits): its partials finish in
+    the reduction kernel, which finds each thread's tensor from the tile
+    counts. Every tensor within the row bar of the oracle and bit-identical
+    to the same tensor launched alone."""
+    rows, cols = [1030, 100, 7], 3584
+    raws = [qmv.synth_tensor(t, r, cols, seed=380 + i) for i, r in enumerate(rows)]
+    dts = [qmv.DeviceTensor(qmv.make_view(raw, t, r, cols)) for raw, r in zip(raws, rows)]
+    x = qmv.synth_normal(batch * cols, seed=383).reshape(batch, cols)
+    dx = hip.DeviceBuffer.from_array(x)
+    s = hip.Stream()
+    grouped = [hip.DeviceBuffer(4 * batch * r) for r in rows]
+    alone = [hip.DeviceBuffer(4 * batch * r) for r in rows]
+    qmv.device_matvec_group(dts, dx.ptr, batch, [y.ptr for y in grouped], s.handle)
+    for dt, y in zip(dts, alone):
+        dt.matvec(dx.ptr, batch, y.ptr, s.handle)
+    s.synchronize()
+    for raw, r, yg, ya in zip(raws, rows, grouped, alone):
+        a = yg.to_array(np.float32, (batch, r))
+        assert np.array_equal(_bits(a), _bits(ya.to_array(np.float32, (batch, r)))), f"{r} rows"
+        _check(oracle, raw, t, r, cols, x, a, f"type {t} group member {r}x{cols} B={batch}")
+    for dt in dts:
+        dt.close()
+
+
 def test_prefill_graph_replay(qmv, gpu, hip):
     t, rows, cols, batch = B.Q6_K, 3584, 18944, 32
     raw = qmv.synth_tensor(t, rows, cols, seed=340)
