@@ -124,8 +124,8 @@ def host_cpus():
 
 def cpu_threads():
     """Threads for the CPU baseline: OMP_NUM_THREADS where the environment
-    sets it (the GPU box's CPU share), else every physical core this process
-    may use."""
+    sets it (a shared machine's CPU share for this job), else every physical
+    core this process may use."""
     env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
     return env if env > 0 else host_cpus()[1]
 
