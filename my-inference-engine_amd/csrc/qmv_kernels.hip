@@ -2045,6 +2045,24 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
     for (int g = 0; g < 4; ++g) b[g] = q4_codes_bf16(q[0][g].x, q[0][g].y, false);
     f32x4_t dp[P][4];
     float sp[4];
+    /* One position block: the activation fragments of sub-block sb + 1 are
+     * read from LDS during step sb, as in q6k_unit_pf (gate|up at 16
+     * positions 34.1 -> 32.2 µs in a cold graph of its launches, the
+     * 16-position decode set 2.582 -> 2.572 ms). Two blocks keep the reads
+     * in the step: the
+     * 24 more VGPRs take the kernel from 248 to 267 and to one wave per SIMD
+     * (gate|up at 32 positions 47.2 -> 60.0 µs). */
+    constexpr bool kAhead = P == 1;
+    typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
+    bf16x8_t fa[P][3], fn[P][3];
+    if constexpr (kAhead) {
+#pragma unroll
+        for (int pb = 0; pb < P; ++pb) {
+            const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
+#pragma unroll
+            for (int l = 0; l < 3; ++l) fa[pb][l] = *(lds_a *)(la + L::offset(l, pb, 0));
+        }
+    }
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         const bool high = sb & 1;
@@ -2077,11 +2095,20 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
         f32x4_t d[P][4];
 #pragma unroll
         for (int pb = 0; pb < P; ++pb) {
-            typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
-            const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
-            const bf16x8_t a0 = *(lds_a *)(la + L::offset(0, pb, sb));
-            const bf16x8_t a1 = *(lds_a *)(la + L::offset(1, pb, sb));
-            const bf16x8_t a2 = *(lds_a *)(la + L::offset(2, pb, sb));
+            bf16x8_t a0, a1, a2;
+            if constexpr (kAhead) {
+                a0 = fa[pb][0];
+                a1 = fa[pb][1];
+                a2 = fa[pb][2];
+                if (sb + 1 < 8)
+#pragma unroll
+                    for (int l = 0; l < 3; ++l) fn[pb][l] = *(lds_a *)(lds + lane * 16 + L::offset(l, pb, sb + 1));
+            } else {
+                const lds_u8 *la = lds + lds_off_after(lane * 16, acc[pb][3][3]);
+                a0 = *(lds_a *)(la + L::offset(0, pb, sb));
+                a1 = *(lds_a *)(la + L::offset(1, pb, sb));
+                a2 = *(lds_a *)(la + L::offset(2, pb, sb));
+            }
 #pragma unroll
             for (int g = 0; g < 4; ++g) d[pb][g] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -2108,6 +2135,11 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
 #pragma unroll
             for (int pb = 0; pb < P; ++pb) dp[pb][g] = d[pb][g];
         }
+        if constexpr (kAhead)
+#pragma unroll
+            for (int pb = 0; pb < P; ++pb)
+#pragma unroll
+                for (int l = 0; l < 3; ++l) fa[pb][l] = fn[pb][l];
     }
 #pragma unroll
     for (int pb = 0; pb < P; ++pb)
