@@ -20,6 +20,7 @@ Configurations:
          projection + greedy argmax
   c5m8   Qwen2.5-7B-shaped decode-step set (28 layers, 4 launches each), 8
          positions per launch
+  c5m32  the same set at 32 positions per launch (one prefill chunk of 32)
 
 Usage: python3 my-inference-engine_amd/config_bench.py [--config c1,c2,...|all] [--reps N]
 Prints one JSON object per configuration.
@@ -49,6 +50,7 @@ def configs():
         "c3": (8, 1, l15),
         "c4": (1, 1, [[("output", Q6_K, 151936, 3584)]]),
         "c5m8": (8, 28, l7),
+        "c5m32": (32, 28, l7),
     }
 
 
