@@ -2049,9 +2049,8 @@ __device__ __forceinline__ void q4k_unit_pf(const uint8_t *slab, const uint8_t *
      * read from LDS during step sb, as in q6k_unit_pf (gate|up at 16
      * positions 34.1 -> 32.2 µs in a cold graph of its launches, the
      * 16-position decode set 2.582 -> 2.572 ms). Two blocks keep the reads
-     * in the step: the
-     * 24 more VGPRs take the kernel from 248 to 267 and to one wave per SIMD
-     * (gate|up at 32 positions 47.2 -> 60.0 µs). */
+     * in the step: the 24 more VGPRs take the kernel from 248 to 267 and to
+     * one wave per SIMD (gate|up at 32 positions 47.2 -> 60.0 µs). */
     constexpr bool kAhead = P == 1;
     typedef __attribute__((address_space(3))) const bf16x8_t lds_a;
     bf16x8_t fa[P][3], fn[P][3];
